@@ -1,0 +1,124 @@
+/*
+ * MI355X (gfx950) split-K decode attention over vLLM's int8 per-token-head paged KV cache.
+ *
+ * C ABI of libpthdec.so. Plain pointers, strides and sizes only; every device pointer is
+ * owned by the caller and no entry point allocates, frees or synchronises the host, so a
+ * launch may be captured in a HIP graph.
+ *
+ * Cache row layout (one row per (block, slot, kv head), 520 bytes):
+ *     [ K int8 x 256 | k_scale f32 | V int8 x 256 | v_scale f32 ]
+ * key_cache is the int8 view [blocks, block_size, Hkv, 260] whose last dim is contiguous;
+ * value_cache is the same storage shifted by 260 bytes; k_scale / v_scale are f32 views
+ * [blocks, block_size, Hkv] at +256 / +516 bytes of each row.
+ *
+ * Reference interfaces replaced (paths relative to the 0c33/mi50-vllm-lab tree):
+ *   pth_dec_launch             <- kernels/pth_dec/pth_dec.cu:285-314 (same signature)
+ *   pth_dec_launch_window      <- same, plus the window / non-causal rule of
+ *                                 patches/vllm/gfx906_fa_paged.patch:7-20 and
+ *                                 kernels/fa_pth/kernel/fattn-q8-paged.cuh:219-229
+ *   pth_dec_supported_layout   <- supported_layout, kernels/pth_dec/pth_dec.cpp:25-41
+ *   pth_dec_decode             <- decode, kernels/pth_dec/pth_dec.cpp:43-91 (the torch op body,
+ *                                 with tensors passed as pd_tensor descriptors)
+ */
+#ifndef PTH_DEC_H
+#define PTH_DEC_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes used in pd_tensor.dtype */
+#define PD_DTYPE_INT8 1
+#define PD_DTYPE_FP16 2
+#define PD_DTYPE_FP32 3
+#define PD_DTYPE_INT32 4
+
+#define PD_MAX_DIMS 4
+
+/* A strided tensor view: data pointer, dtype code, rank, sizes and strides in elements. */
+typedef struct pd_tensor {
+    const void* data;
+    int32_t dtype;
+    int32_t ndim;
+    int64_t sizes[PD_MAX_DIMS];
+    int64_t strides[PD_MAX_DIMS];
+} pd_tensor;
+
+/*
+ * Split-K decode attention, causal, no window. Same arguments, meaning and error codes as
+ * kernels/pth_dec/pth_dec.cu:285-290:
+ *   q            fp16 [num_tokens, heads_q, 256], token stride q_st elements, head stride 256
+ *   kc           int8 cache base (key_cache.data_ptr()); k_sb / k_ss / k_sh are the byte strides
+ *                of blocks, slots and kv heads; V sits at +260 bytes of each K row
+ *   block_table  int32, row stride bt_stride; seq_lens int32 [num_seqs];
+ *   qsl          int32 query_start_loc [num_seqs + 1]
+ *   part_o       fp32 [>= num_tokens, heads_q, nseg, 256]; part_m / part_l fp32 [.., heads_q, nseg]
+ *   out          fp16, element (t, h, d) at out + t * o_st + h * o_sh + d
+ * Returns hipErrorInvalidValue unless heads_q == 6 * heads_kv, 1 <= qmax <= 4,
+ * 1 <= nsplit <= nseg and num_seqs >= 1.
+ */
+hipError_t pth_dec_launch(const void* q, int q_st, const void* kc, int k_sb, int k_ss, int k_sh,
+                          const int* block_table, int bt_stride, const int* seq_lens, const int* qsl,
+                          int num_seqs, int num_tokens, int heads_q, int heads_kv, int block_size,
+                          float scale, int qmax, float* part_o, float* part_m, float* part_l, int nseg,
+                          int nsplit, void* out, long o_st, long o_sh, hipStream_t stream);
+
+/*
+ * pth_dec_launch with the arguments the DFlash2 drafter needs appended:
+ *   window  > 0: row j of a sequence (absolute position p_j = seq_len - q_len + j) sees key k
+ *                only if p_j - k < window; <= 0 (e.g. -1): no window
+ *   causal  != 0: key k > p_j is masked; 0: every key < seq_len is visible (non-causal block)
+ * Any GQA ratio heads_q / heads_kv with qmax * (heads_q / heads_kv) <= 48 is accepted
+ * (MTP 4 x 6 = 24 rows, DFlash2 8 x 6 = 48 rows).
+ */
+hipError_t pth_dec_launch_window(const void* q, int q_st, const void* kc, int k_sb, int k_ss, int k_sh,
+                                 const int* block_table, int bt_stride, const int* seq_lens,
+                                 const int* qsl, int num_seqs, int num_tokens, int heads_q, int heads_kv,
+                                 int block_size, float scale, int qmax, float* part_o, float* part_m,
+                                 float* part_l, int nseg, int nsplit, void* out, long o_st, long o_sh,
+                                 hipStream_t stream, int window, int causal);
+
+/*
+ * The two stages of pth_dec_launch_window launched separately (no counterpart in the
+ * reference, which always launches both): the split-K partial pass writes part_o / part_m /
+ * part_l, the combine pass merges them into out. Same argument checks.
+ */
+hipError_t pth_dec_launch_partial(const void* q, int q_st, const void* kc, int k_sb, int k_ss, int k_sh,
+                                  const int* block_table, int bt_stride, const int* seq_lens,
+                                  const int* qsl, int num_seqs, int num_tokens, int heads_q,
+                                  int heads_kv, int block_size, float scale, int qmax, float* part_o,
+                                  float* part_m, float* part_l, int nseg, int nsplit,
+                                  hipStream_t stream, int window, int causal);
+hipError_t pth_dec_launch_combine(const int* seq_lens, const int* qsl, int num_seqs, int num_tokens,
+                                  int heads_q, int qmax, const float* part_o, const float* part_m,
+                                  const float* part_l, int nseg, int nsplit, void* out, long o_st,
+                                  long o_sh, hipStream_t stream);
+
+/* 1 if the four cache views have the row layout above, else 0 (pth_dec.cpp:25-41). */
+int pth_dec_supported_layout(const pd_tensor* key_cache, const pd_tensor* value_cache,
+                             const pd_tensor* k_scale, const pd_tensor* v_scale);
+
+/*
+ * The torch op `decode` of kernels/pth_dec/pth_dec.cpp:49-91 over descriptors, with window
+ * and causal appended. Validates every tensor like the reference's TORCH_CHECKs; on failure
+ * returns 1 and writes the reference's message into err (errlen bytes, NUL-terminated);
+ * returns 2 with the HIP error string if the launch fails; 0 on success.
+ */
+int pth_dec_decode(const pd_tensor* q, const pd_tensor* key_cache, const pd_tensor* value_cache,
+                   const pd_tensor* k_scale, const pd_tensor* v_scale, const pd_tensor* block_table,
+                   const pd_tensor* seq_lens, const pd_tensor* query_start_loc, const pd_tensor* out,
+                   double scale, const pd_tensor* part_o, const pd_tensor* part_m, const pd_tensor* part_l,
+                   int64_t num_seqs, int64_t qmax, int64_t nsplit, int64_t window, int64_t causal,
+                   hipStream_t stream, char* err, int errlen);
+
+/* Library version string. */
+const char* pth_dec_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PTH_DEC_H */

@@ -1,0 +1,61 @@
+"""Build libpthdec.so (gfx950) in-tree with hipcc.
+
+    python mi50-vllm-lab_amd/build.py [--save-temps DIR]
+
+The library is the C ABI declared in include/pth_dec.h. It is always rebuilt: hipcc takes
+about half a minute and a stale library is worse than a slow build.
+"""
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB_DIR = os.path.join(HERE, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libpthdec.so")
+SOURCES = [os.path.join(HERE, "csrc", "pth_dec.hip")]
+ARCH = "gfx950"
+
+# Packed-FP32 VALU forms are disabled for all device code built here.
+HIP_FLAGS = [
+    "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-fPIC", "-shared",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build libpthdec.so)")
+
+
+def build(save_temps: str | None = None, verbose: bool = False) -> str:
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = LIB_PATH + ".tmp"
+    cmd = [hipcc(), *HIP_FLAGS, "-I", os.path.join(ROOT, "include"), *SOURCES, "-o", tmp]
+    if save_temps:
+        os.makedirs(save_temps, exist_ok=True)
+        cmd.insert(1, f"-save-temps={'obj'}")
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    cwd = save_temps if save_temps else None
+    if save_temps:
+        cmd[-1] = os.path.abspath(tmp)
+    res = subprocess.run(cmd, cwd=cwd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"hipcc failed ({res.returncode}) building {LIB_PATH}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--save-temps", default=None, help="directory for hipcc -save-temps output")
+    ap.add_argument("-v", "--verbose", action="store_true")
+    args = ap.parse_args()
+    print(build(args.save_temps, args.verbose))

@@ -1,0 +1,184 @@
+"""Python face of libpthdec.so: the `_gfx906_pth_dec` torch-op interface, re-targeted at gfx950.
+
+`decode` and `supported_layout` keep the names, argument order, meaning and error behaviour of
+the reference torch extension (kernels/pth_dec/pth_dec.cpp:27-28,49-53,93-95): every check of
+the reference's TORCH_CHECKs raises RuntimeError with the same message, the op allocates
+nothing and launches on torch's current stream, so it is safe inside HIP-graph capture.
+`decode` additionally takes `window` (<= 0: none) and `causal` (the DFlash2 drafter's
+non-causal sliding-window rows, patches/vllm/gfx906_fa_paged.patch:7-20).
+
+Tensors cross the C ABI as `pd_tensor` descriptors (data pointer, dtype code, sizes, strides);
+no torch type appears in the ABI. The library has no CPU fallback: if it is not built, every
+entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("PTH_DEC_LIB", os.path.join(_HERE, "lib", "libpthdec.so"))
+
+PD_DTYPE_INT8 = 1
+PD_DTYPE_FP16 = 2
+PD_DTYPE_FP32 = 3
+PD_DTYPE_INT32 = 4
+PD_MAX_DIMS = 4
+
+_DTYPES = {
+    torch.int8: PD_DTYPE_INT8,
+    torch.float16: PD_DTYPE_FP16,
+    torch.float32: PD_DTYPE_FP32,
+    torch.int32: PD_DTYPE_INT32,
+}
+
+# Every symbol include/pth_dec.h declares.
+EXPORTED_SYMBOLS = (
+    "pth_dec_launch",
+    "pth_dec_launch_window",
+    "pth_dec_launch_partial",
+    "pth_dec_launch_combine",
+    "pth_dec_supported_layout",
+    "pth_dec_decode",
+    "pth_dec_version",
+)
+
+
+class PdTensor(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("ndim", ctypes.c_int32),
+        ("sizes", ctypes.c_int64 * PD_MAX_DIMS),
+        ("strides", ctypes.c_int64 * PD_MAX_DIMS),
+    ]
+
+
+_lib = None
+
+
+def load_library(path: str | None = None) -> ctypes.CDLL:
+    """Load libpthdec.so (once) and declare the C signatures. Raises if it is not built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = path or LIB_PATH
+    if not os.path.exists(p):
+        raise RuntimeError(f"libpthdec.so not found at {p}; build it with mi50-vllm-lab_amd/build.py")
+    lib = ctypes.CDLL(p)
+    c_int, c_long, c_float, c_double, vp = ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_double, ctypes.c_void_p
+    ip = ctypes.POINTER(ctypes.c_int)
+    fp = ctypes.POINTER(ctypes.c_float)
+    launch_args = [vp, c_int, vp, c_int, c_int, c_int, ip, c_int, ip, ip, c_int, c_int, c_int, c_int, c_int,
+                   c_float, c_int, fp, fp, fp, c_int, c_int, vp, c_long, c_long, vp]
+    lib.pth_dec_launch.argtypes = launch_args
+    lib.pth_dec_launch.restype = c_int
+    lib.pth_dec_launch_window.argtypes = launch_args + [c_int, c_int]
+    lib.pth_dec_launch_window.restype = c_int
+    lib.pth_dec_launch_partial.argtypes = [vp, c_int, vp, c_int, c_int, c_int, ip, c_int, ip, ip, c_int, c_int,
+                                           c_int, c_int, c_int, c_float, c_int, fp, fp, fp, c_int, c_int, vp,
+                                           c_int, c_int]
+    lib.pth_dec_launch_partial.restype = c_int
+    lib.pth_dec_launch_combine.argtypes = [ip, ip, c_int, c_int, c_int, c_int, fp, fp, fp, c_int, c_int, vp,
+                                           c_long, c_long, vp]
+    lib.pth_dec_launch_combine.restype = c_int
+    tp = ctypes.POINTER(PdTensor)
+    lib.pth_dec_supported_layout.argtypes = [tp, tp, tp, tp]
+    lib.pth_dec_supported_layout.restype = c_int
+    lib.pth_dec_decode.argtypes = [tp] * 9 + [c_double, tp, tp, tp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                              ctypes.c_int64, ctypes.c_int64, vp, ctypes.c_char_p, c_int]
+    lib.pth_dec_decode.restype = c_int
+    lib.pth_dec_version.argtypes = []
+    lib.pth_dec_version.restype = ctypes.c_char_p
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def describe(t: torch.Tensor) -> PdTensor:
+    """pd_tensor descriptor of a strided tensor (no copy)."""
+    if t.dim() > PD_MAX_DIMS:
+        raise RuntimeError(f"tensor rank {t.dim()} exceeds {PD_MAX_DIMS}")
+    d = PdTensor()
+    d.data = t.data_ptr()
+    d.dtype = _DTYPES.get(t.dtype, 0)
+    d.ndim = t.dim()
+    for i in range(t.dim()):
+        d.sizes[i] = t.size(i)
+        d.strides[i] = t.stride(i)
+    return d
+
+
+def supported_layout(key_cache: torch.Tensor, value_cache: torch.Tensor, k_scale: torch.Tensor,
+                     v_scale: torch.Tensor) -> bool:
+    """True if the cache views have vLLM's int8 per-token-head row layout
+    [K 256 | k_scale f32 | V 256 | v_scale f32] (kernels/pth_dec/pth_dec.cpp:25-41)."""
+    lib = load_library()
+    descs = [describe(t) for t in (key_cache, value_cache, k_scale, v_scale)]
+    return bool(lib.pth_dec_supported_layout(*[ctypes.byref(x) for x in descs]))
+
+
+def decode(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, k_scale: torch.Tensor,
+           v_scale: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor,
+           query_start_loc: torch.Tensor, out: torch.Tensor, scale: float, part_o: torch.Tensor,
+           part_m: torch.Tensor, part_l: torch.Tensor, num_seqs: int, qmax: int, nsplit: int,
+           window: int = -1, causal: bool = True) -> None:
+    """Split-K decode attention over the int8 per-token-head paged KV cache, written into `out`.
+
+    q: fp16 [T, Hq, 256] with head stride 256; out: fp16 [T, Hq, 256] with unit dim stride;
+    block_table int32 [>= num_seqs, max_blocks]; seq_lens int32 [>= num_seqs];
+    query_start_loc int32 [>= num_seqs + 1]; every sequence has <= qmax query tokens;
+    part_o fp32 [>= T, Hq, NSEG, 256], part_m / part_l fp32 [>= T, Hq, NSEG] (caller-owned
+    scratch, vLLM's softmax segment buffers); 1 <= nsplit <= NSEG.
+    Reference: kernels/pth_dec/pth_dec.cpp:43-91.
+    """
+    if not q.is_cuda:
+        raise RuntimeError("q must be fp16 [T, Hq, 256] with contiguous heads")
+    lib = load_library()
+    tensors = (q, key_cache, value_cache, k_scale, v_scale, block_table, seq_lens, query_start_loc, out)
+    descs = [describe(t) for t in tensors]
+    pdescs = [describe(t) for t in (part_o, part_m, part_l)]
+    err = ctypes.create_string_buffer(256)
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        rc = lib.pth_dec_decode(*[ctypes.byref(x) for x in descs], float(scale),
+                                *[ctypes.byref(x) for x in pdescs], int(num_seqs), int(qmax), int(nsplit),
+                                int(window), 1 if causal else 0, ctypes.c_void_p(stream), err, len(err))
+    if rc != 0:
+        raise RuntimeError(err.value.decode())
+
+
+def _ptr(t: torch.Tensor, ctype):
+    return ctypes.cast(ctypes.c_void_p(t.data_ptr()), ctypes.POINTER(ctype))
+
+
+def launch_partial(q, key_cache, block_table, seq_lens, query_start_loc, part_o, part_m, part_l, *,
+                   num_seqs: int, heads_q: int, heads_kv: int, block_size: int, scale: float, qmax: int,
+                   nsplit: int, window: int = -1, causal: bool = True, stream=None) -> int:
+    """Raw C-ABI call of the split-K partial pass (pth_dec_launch_partial); returns the hipError_t."""
+    lib = load_library()
+    s = stream if stream is not None else torch.cuda.current_stream(q.device).cuda_stream
+    return lib.pth_dec_launch_partial(
+        ctypes.c_void_p(q.data_ptr()), q.stride(0), ctypes.c_void_p(key_cache.data_ptr()),
+        key_cache.stride(0), key_cache.stride(1), key_cache.stride(2), _ptr(block_table, ctypes.c_int),
+        block_table.stride(0), _ptr(seq_lens, ctypes.c_int), _ptr(query_start_loc, ctypes.c_int), num_seqs,
+        q.size(0), heads_q, heads_kv, block_size, scale, qmax, _ptr(part_o, ctypes.c_float),
+        _ptr(part_m, ctypes.c_float), _ptr(part_l, ctypes.c_float), part_o.size(2), nsplit,
+        ctypes.c_void_p(s), window, 1 if causal else 0)
+
+
+def launch_combine(seq_lens, query_start_loc, part_o, part_m, part_l, out, *, num_seqs: int, qmax: int,
+                   nsplit: int, stream=None) -> int:
+    """Raw C-ABI call of the log-sum-exp combine pass (pth_dec_launch_combine)."""
+    lib = load_library()
+    s = stream if stream is not None else torch.cuda.current_stream(out.device).cuda_stream
+    return lib.pth_dec_launch_combine(
+        _ptr(seq_lens, ctypes.c_int), _ptr(query_start_loc, ctypes.c_int), num_seqs, out.size(0), out.size(1),
+        qmax, _ptr(part_o, ctypes.c_float), _ptr(part_m, ctypes.c_float), _ptr(part_l, ctypes.c_float),
+        part_o.size(2), nsplit, ctypes.c_void_p(out.data_ptr()), out.stride(0), out.stride(1), ctypes.c_void_p(s))
+
+
+def version() -> str:
+    return load_library().pth_dec_version().decode()
