@@ -11,30 +11,31 @@
 //   every 4th tile. All R = q_len * G query rows of the GQA group (24 for MTP, 48 for
 //   DFlash2) are held as 16-row blocks, so one read of a K/V tile serves every row.
 //
-// Memory path: HBM -> LDS by DMA (global_load_lds_dwordx4), double-buffered per wave.
-//   Each lane owns one key row of the tile (rows are 520 bytes, 8-byte aligned) and issues
-//   17 16-byte DMAs for it: 8 for the K bytes, 9 for row bytes [248, 520) (k_scale, V,
-//   v_scale). The tile's image lands in LDS chunk-major ([chunk][row][16 B]) so every later
-//   LDS read is bank-conflict free, and no VGPR ever holds data in flight. The next tile's
-//   DMAs are issued before the current tile is computed; s_waitcnt vmcnt(17) waits for the
-//   current one only. The block-table entries of a tile are read with scalar loads one tile
-//   ahead.
+// Memory path: HBM -> LDS by DMA (global_load_lds_dwordx4), double-buffered per wave, no VGPR
+//   holding data in flight. One DMA instruction moves two whole key rows (lanes 0-31: bytes
+//   [0, 512) of row 2i, lanes 32-63: of row 2i+1; 512 contiguous bytes per half-wave), 16
+//   instructions per tile plus one for bytes [504, 520) of each row. With block_size 16 or
+//   >= 32 (even) both rows of a pair sit in one page, so every instruction is addressed by a
+//   scalar base (page, slot: scalar ALU) and a per-lane constant offset: no vector ALU per DMA.
+//   The next tile's DMAs are issued before the current tile is computed; s_waitcnt vmcnt
+//   waits for the current one only. The block-table slice of the split is staged in LDS once.
 //
 // Per 32-key tile, per wave
 //   S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims of K (int8 widened to fp16
-//     exactly: 0x6400|(b^0x80) encodes 1024+b+128), B = Q^T held in registers.
-//   softmax: base 2, fp32, online; per-row max = in-lane max + two cross-lane exchanges. The
-//     running max of a row is raised only when a tile exceeds it by > 2^4 (rare after the
-//     first tile), so O is rarely rescaled; P' = p * v_scale * 16 in fp16 has the same range as
-//     p * v_scale * 256 with p <= 1. Masked weights are chosen by select, so a NaN scale on a
-//     masked row cannot leak in.
-//   O^T += V^T P^T: ds_read_b64_tr_b8 hands each lane 8 keys of one V column (the A operand,
+//     exactly: 0x6400|(b^0x80) encodes 1024+b+128), B = Q^T held in registers; the four
+//     accumulation chains (2 key blocks x 2 row blocks) are interleaved.
+//   softmax: base 2, fp32, online. A row's running max is raised only when a tile exceeds it
+//     by > 2^4: each lane tests its own 8 scores and one ballot decides; only then is the row
+//     max reduced across lanes and O rescaled (rare after the first tile). P' = p * v_scale * 16
+//     in fp16 has the range of p * v_scale * 256 with p <= 1. Masked weights are chosen by
+//     select, so a NaN scale on a masked row cannot leak in.
+//   O^T += V^T P^T: ds_read_b64_tr_b8 hands each lane 8 keys of one V column (A operand,
 //     16 dims x 32 keys); P^T never leaves registers: the S^T accumulator layout (lane = query
-//     row, 4 keys per 16-key block) is the B-operand layout once the MFMA's key order is
-//     chosen to match. The V image starts 12 bytes before V[0], so 17 16-dim blocks cover the
-//     256 dims; the lanes that fall outside [0, 256) are discarded.
-//   Keys outside [lo, seq_len) are never addressed: their row pointers are clamped onto the
-//     first / last visible key, so block-table entries of freed pages are never read.
+//     row, 4 keys per 16-key block) is the B-operand layout once the MFMA's key order is chosen
+//     to match. Dim block j < 16 reads row bytes [256 + 16 j, 272 + 16 j) (dims 16 j - 4 ..),
+//     block 16 the tail bytes (dims 244..255); lanes outside [0, 256) are discarded.
+//   Keys outside [lo, seq_len) are never addressed through freed pages: rows of a tile that
+//     fall outside are pointed at a page the split can see and masked.
 //
 // End of split: the 4 waves merge (m, l, O) through LDS and write one partial per row:
 //   part_o [T, Hq, nseg, 256] unnormalised, part_m [T, Hq, nseg] running max in log2 units,
@@ -48,6 +49,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "pth_dec.h"
 
 namespace {
@@ -60,12 +63,11 @@ typedef __attribute__((address_space(3))) unsigned char lds_u8;
 typedef __attribute__((address_space(3))) int2_t lds_int2;
 typedef __attribute__((address_space(3))) uint4_t lds_uint4;
 typedef __attribute__((address_space(3))) float lds_float;
+typedef __attribute__((address_space(3))) int lds_int;
 typedef const __attribute__((address_space(4))) int* const_int_ptr;  // scalar-cache loads
 
 constexpr int kDim = 256;             // head dim (the only one the cache row layout allows)
-constexpr int kTile = 32;             // keys per wave tile
-constexpr int kWaves = 4;             // waves per workgroup
-constexpr int kThreads = 64 * kWaves;
+constexpr int kTile = 32;             // keys per tile
 constexpr int kMaxRowBlocks = 3;      // up to 48 query rows per kv head
 constexpr float kNegInf = -__builtin_inff();
 // The running max m of a row is only raised when a tile's max exceeds it by more than
@@ -74,21 +76,16 @@ constexpr float kNegInf = -__builtin_inff();
 constexpr float kLazy = 4.0f;
 constexpr float kPScale = 16.0f;
 
-// LDS image of one tile: K [16 chunks][32 rows][16 B], then V [18 pos][32 rows][16 B] where
-// pos p holds row bytes [248 + 16 p, 264 + 16 p) (pos 17 repeats pos 16).
-constexpr int kKBytes = 16 * kTile * 16;
-constexpr int kVFirst = 248;
-constexpr int kVBytes = 18 * kTile * 16;
-constexpr int kTileBytes = kKBytes + kVBytes;
-constexpr int kWaveBytes = 2 * kTileBytes;              // double buffer
-constexpr int kLdsTiles = kWaves * kWaveBytes;
-constexpr int kOPitch = kDim + 4;                       // floats per row of the merge buffer
-constexpr int kLdsMerge = kWaves * 16 * kOPitch * 4;    // aliases the tile buffers
-constexpr int kLdsStats = kLdsTiles;
-constexpr int kLdsBytes = kLdsStats + 2 * kWaves * 16 * kMaxRowBlocks * 4;
-constexpr int kDmaPerTile = 17;
-static_assert(kLdsMerge <= kLdsTiles, "merge buffer must fit in the tile buffers");
-static_assert(kLdsBytes <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
+// LDS image of one tile: 16 blocks of two rows (2i, 2i+1) kPair bytes apart, row r's bytes
+// [0, 512) at row_ofs(r) (the 16-byte gap between blocks spreads the LDS banks), then the
+// tail block: row r's bytes [504, 520) at kTailOfs + 16 r (lanes 32-63 land a copy behind).
+constexpr int kPair = 1040;
+constexpr int kTailOfs = 16 * kPair;
+constexpr int kTileBytes = kTailOfs + 1024;
+constexpr int kOPitch = kDim + 4;     // floats per row of the merge buffer
+constexpr int kBtCache = 1024;        // block-table entries of a split kept in LDS
+
+__device__ __forceinline__ int row_ofs(int r) { return (r >> 1) * kPair + (r & 1) * 512; }
 
 struct PartialParams {
     const _Float16* q;
@@ -127,7 +124,12 @@ struct CombineParams {
     int qmax;
 };
 
-// 8 signed bytes (two dwords, byte 0 first) -> 8 fp16, exact.
+
+// 8 signed bytes b (two dwords, byte 0 first) -> 8 fp16 holding b + 1152, exact: the bit
+// pattern 0x6400 | (b ^ 0x80) encodes 1024 + (b + 128). The constant 1152 is not subtracted
+// here; the kernel removes it once per row instead: S = sum_d q_d (k_d + 1152) - 1152 sum_d q_d
+// and O = sum_k P'_k (v_k + 1152) - 1152 sum_k P'_k.
+constexpr float kWidenBias = 1152.0f;
 __device__ __forceinline__ half8_t widen_i8x8(unsigned w0, unsigned w1) {
     const unsigned u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;  // b + 128 as unsigned bytes
     // v_perm_b32 selector bytes 0..3 pick bytes of the 2nd operand, 4 picks byte 0 of the 1st.
@@ -136,119 +138,133 @@ __device__ __forceinline__ half8_t widen_i8x8(unsigned w0, unsigned w1) {
     h.y = __builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u);  // [u0.b2, 0x64, u0.b3, 0x64]
     h.z = __builtin_amdgcn_perm(0x64646464u, u1, 0x04010400u);
     h.w = __builtin_amdgcn_perm(0x64646464u, u1, 0x04030402u);
-    return __builtin_bit_cast(half8_t, h) - (_Float16)1152.0f;
+    return __builtin_bit_cast(half8_t, h);
 }
 
 __device__ __forceinline__ float xor_max(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, 64)); }
 __device__ __forceinline__ float xor_sum(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
 
-// One 16-byte HBM -> LDS DMA per lane: LDS[m0 + IMM + 16 * lane] = global[g + IMM .. + 16).
-// Issued through asm so the compiler does not add its conservative vmcnt(0) before every LDS
-// read; completion is awaited explicitly with wait_vm.
-template <int IMM>
-__device__ __forceinline__ void dma16(const int8_t* g, unsigned m0) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off offset:%2" ::"v"(g), "s"(m0), "i"(IMM)
+// 16-byte HBM -> LDS DMAs: LDS[m0 + 16 * lane] = global[...]. Issued through asm so the
+// compiler does not add its conservative vmcnt(0) before every LDS read; completion is awaited
+// explicitly with wait_vm. dma16_s: scalar base + per-lane 32-bit offset; dma16_v: per-lane address.
+__device__ __forceinline__ void dma16_s(const int8_t* sbase, unsigned voff, unsigned m0) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0)
                  : "memory", "m0");
 }
-// If do_scale (wave-uniform, nonzero): acc *= alpha, for an MFMA accumulator kept in AGPRs.
-// The test and the multiply are both inside the asm so that, to the compiler, this is an
-// in-place update with no control flow: a C-level branch makes the register allocator copy
-// every accumulator out of the AGPRs on each loop iteration although the rescale is rare.
-__device__ __forceinline__ void scale_acc_if(float4_t& acc, float alpha, int do_scale) {
-    float a0 = acc[0], a1 = acc[1], a2 = acc[2], a3 = acc[3];
-    float t;
-    asm volatile(
-        "s_cmp_eq_u32 %6, 0\n\t"
-        "s_cbranch_scc1 .Lpd_skip_%=\n\t"
-        "v_accvgpr_read_b32 %4, %0\n\tv_mul_f32 %4, %4, %5\n\tv_accvgpr_write_b32 %0, %4\n\t"
-        "v_accvgpr_read_b32 %4, %1\n\tv_mul_f32 %4, %4, %5\n\tv_accvgpr_write_b32 %1, %4\n\t"
-        "v_accvgpr_read_b32 %4, %2\n\tv_mul_f32 %4, %4, %5\n\tv_accvgpr_write_b32 %2, %4\n\t"
-        "v_accvgpr_read_b32 %4, %3\n\tv_mul_f32 %4, %4, %5\n\tv_accvgpr_write_b32 %3, %4\n\t"
-        "s_nop 1\n"
-        ".Lpd_skip_%=:"
-        : "+a"(a0), "+a"(a1), "+a"(a2), "+a"(a3), "=&v"(t)
-        : "v"(alpha), "s"(do_scale)
-        : "scc");
-    acc = float4_t{a0, a1, a2, a3};
+__device__ __forceinline__ void dma16_v(const int8_t* vaddr, unsigned m0) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(vaddr), "s"(m0) : "memory", "m0");
 }
-
 template <int N>
 __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// The 17 DMAs of one tile for this lane's key row. kofs / vofs: LDS addresses of the tile's
-// K and V images. Lanes h = 0 / 1 fetch alternate 16-byte chunks of the same row.
-__device__ __forceinline__ void issue_tile(const int8_t* row, int h, unsigned kofs, unsigned vofs) {
-    const int8_t* gh = row + 16 * h;
-    // K: chunk 2i + h at LDS kofs + 512 (2i + h) + 16 row = m0 + imm + 16 lane
-#define PD_K(i) dma16<32 * (i)>(gh, kofs + 1024u * (i) - 32u * (i))
-    PD_K(0); PD_K(1); PD_K(2); PD_K(3); PD_K(4); PD_K(5); PD_K(6); PD_K(7);
-#undef PD_K
-    // V image pos 2i + h: row bytes [248 + 32 i + 16 h, +16)
-#define PD_V(i) dma16<kVFirst + 32 * (i)>(gh, vofs + 1024u * (i) - (unsigned)(kVFirst + 32 * (i)))
-    PD_V(0); PD_V(1); PD_V(2); PD_V(3); PD_V(4); PD_V(5); PD_V(6); PD_V(7);
-#undef PD_V
-    // pos 16 = row bytes [504, 520); the h = 1 half lands a copy in pos 17
-    dma16<kVFirst + 256>(row, vofs + 8192u - (unsigned)(kVFirst + 256));
-}
-
-// Uniform page lookups of one tile: the (at most two) pages its visible keys live on.
-struct TilePages {
-    int kb, kfirst, klast, lbA, split;
-    int64_t blkA, blkB;
+// Block-table access of one workgroup: the slice of pages its split can touch is staged in
+// LDS when it fits (kBtCache entries), so the tile loop issues no loads of its own besides the
+// K/V DMAs; otherwise entries are read with scalar loads through the constant address space.
+struct PageTable {
+    const lds_int* lds;  // slice [pfirst, pfirst + kBtCache)
+    const_int_ptr glob;  // this sequence's block-table row
+    int pfirst;
+    int in_lds;
+    template <bool kLds>
+    __device__ __forceinline__ int64_t get(int lb) const {
+        if constexpr (kLds)
+            return (int64_t)lds[lb - pfirst];
+        else
+            return (int64_t)glob[lb];
+    }
+    // Same, for a wave-uniform lb: the result is made uniform (scalar register) explicitly.
+    template <bool kLds>
+    __device__ __forceinline__ int64_t get_uniform(int lb) const {
+        if constexpr (kLds)
+            return (int64_t)__builtin_amdgcn_readfirstlane(lds[lb - pfirst]);
+        else
+            return (int64_t)glob[lb];
+    }
 };
 
-template <bool kFastBT>
-__device__ __forceinline__ TilePages tile_pages(const PartialParams& a, const_int_ptr bt_row, int tile, int lo,
-                                                int hi) {
-    TilePages p;
-    p.kb = tile * kTile;
-    p.kfirst = max(p.kb, lo);
-    p.klast = min(p.kb + kTile - 1, hi - 1);
+// The 17 DMAs of one tile into the LDS image at lds_tile. voff_pair = h * k_ss + 16 * (lane & 31).
+// kFastBT (block_size 16, or even and >= 32): a tile's keys span at most two pages and both rows
+// of a pair share a page, so every instruction takes a scalar base. Rows whose key is not
+// visible are pointed at a visible page (their slot's row is read and masked later), so a freed
+// page is never addressed. Otherwise each lane addresses its own row (keys clamped into the
+// visible range) and the pair addresses are exchanged with readlane.
+template <bool kFastBT, bool kLds, int NRB>
+__device__ __forceinline__ void issue_tile(const PartialParams& a, const PageTable& pt, int tile, int lo, int hi,
+                                           int g, int lane, unsigned lds_tile, unsigned voff_pair, int part) {
+    // The NRB waves of a tile group share the 17 DMAs: wave `part` issues i = part, part + NRB, ...
+    const int kb = tile * kTile;
+    const int kfirst = max(kb, lo), klast = min(kb + kTile - 1, hi - 1);
+    const int bs = a.block_size;
+    const int rho = lane & 31, h = lane >> 5;
+    const int8_t* gbase = a.kc + (int64_t)g * a.k_sh;
     if constexpr (kFastBT) {
-        // block_size == 16 or >= 32: a 32-aligned tile touches at most two pages.
-        const int bs = a.block_size;
-        p.lbA = p.kfirst / bs;
-        const int lbB = p.klast / bs;
-        p.blkA = bt_row[p.lbA];
-        p.blkB = bt_row[lbB];
-        p.split = (p.lbA + 1) * bs;
+        const int lbA = kfirst / bs, lbB = klast / bs;  // lbB <= lbA + 1
+        const int8_t* pA = gbase + pt.get_uniform<kLds>(lbA) * a.k_sb;
+        const int8_t* pB = gbase + pt.get_uniform<kLds>(lbB) * a.k_sb;
+        const int lb0 = kb / bs, s0 = kb - lb0 * bs;  // page / slot of the tile's first key
+        // rows before the tile's first page boundary live at bf + key * k_ss, the rest at
+        // bw + key * k_ss (key = 0..31 inside the tile; at most one boundary since bs >= 16)
+        const int8_t* bf = (lb0 > lbA ? pB : pA) + (int64_t)s0 * a.k_ss;
+        const int8_t* bw = (lb0 + 1 > lbA ? pB : pA) - (int64_t)(bs - s0) * a.k_ss;
+        const int64_t k2 = 2 * a.k_ss;
+        for (int i = part; i < 16; i += NRB)
+            dma16_s((s0 + 2 * i < bs ? bf : bw) + (int64_t)i * k2, voff_pair, lds_tile + i * kPair);
+        if (part == 16 % NRB) {
+            int slot = s0 + rho, lb = lb0;
+            if (slot >= bs) {
+                slot -= bs;
+                lb += 1;
+            }
+            dma16_v((lb > lbA ? pB : pA) + (int64_t)slot * a.k_ss + 504, lds_tile + kTailOfs);
+        }
     } else {
-        p.lbA = 0;
-        p.blkA = p.blkB = 0;
-        p.split = 0;
+        const int t = min(max(kb + rho, kfirst), klast);
+        const int lb = t / bs;
+        const int8_t* rowp = gbase + pt.get<kLds>(lb) * a.k_sb + (int64_t)(t - lb * bs) * a.k_ss;
+        const uint64_t ra = (uint64_t)(uintptr_t)rowp;
+        const unsigned lo32 = (unsigned)ra, hi32 = (unsigned)(ra >> 32);
+        for (int i = part; i < 16; i += NRB) {
+            const unsigned l0 = __builtin_amdgcn_readlane(lo32, 2 * i);
+            const unsigned h0 = __builtin_amdgcn_readlane(hi32, 2 * i);
+            const unsigned l1 = __builtin_amdgcn_readlane(lo32, 2 * i + 1);
+            const unsigned h1 = __builtin_amdgcn_readlane(hi32, 2 * i + 1);
+            const uint64_t rr = h ? (((uint64_t)h1 << 32) | l1) : (((uint64_t)h0 << 32) | l0);
+            dma16_v((const int8_t*)(uintptr_t)(rr + 16u * (unsigned)rho), lds_tile + i * kPair);
+        }
+        if (part == 16 % NRB) dma16_v(rowp + 504, lds_tile + kTailOfs);
     }
-    return p;
 }
 
-// Address of this lane's key row (row rho of the tile), clamped into the visible keys.
-template <bool kFastBT>
-__device__ __forceinline__ const int8_t* tile_row(const PartialParams& a, const_int_ptr bt_row, const TilePages& p,
-                                                  int rho, int g) {
-    const int t = min(max(p.kb + rho, p.kfirst), p.klast);
-    int64_t blk;
-    int sl;
-    if constexpr (kFastBT) {
-        const bool inB = t >= p.split;
-        blk = inB ? p.blkB : p.blkA;
-        sl = t - (inB ? p.split : p.lbA * a.block_size);
-    } else {
-        const int lb = t / a.block_size;
-        sl = t - lb * a.block_size;
-        blk = bt_row[lb];
-    }
-    return a.kc + blk * a.k_sb + (int64_t)sl * a.k_ss + (int64_t)g * a.k_sh;
-}
+// Workgroup shape for NRB row blocks: TG tile groups; the NRB waves of a tile group share
+// every tile (one LDS image, DMAs split between them) and each owns one row block, so a wave
+// holds only its own 16 rows of Q and O and two waves run on every SIMD.
+template <int NRB>
+struct Shape {
+    static constexpr int TG = NRB <= 2 ? 4 : 2;
+    static constexpr int kWavesWG = TG * NRB;
+    static constexpr int kThreadsWG = 64 * kWavesWG;
+    static constexpr int kLdsTiles = TG * 2 * kTileBytes;                    // double buffer per group
+    static constexpr int kLdsMerge = NRB * TG * 16 * kOPitch * 4;           // aliases the tiles
+    static constexpr int kLdsUnion = kLdsTiles > kLdsMerge ? kLdsTiles : kLdsMerge;
+    static constexpr int kLdsStats = kLdsUnion;                             // wm / wl [NRB][TG][16]
+    static constexpr int kLdsBt = kLdsStats + 2 * NRB * TG * 16 * 4;
+    static constexpr int kLdsBytes = kLdsBt + kBtCache * 4;
+    static_assert(kLdsBytes <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
+};
 
 template <int NRB, bool kFastBT>
-__global__ void __launch_bounds__(kThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ void __launch_bounds__(Shape<NRB>::kThreadsWG, 1)
 pd_partial_kernel(const PartialParams a) {
-    __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+    using S = Shape<NRB>;
+    constexpr int TG = S::TG;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[S::kLdsBytes];
 
     const int s = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, l = tid & 63, lg = l >> 4, li = l & 15, h = l >> 5;
+    const int tid = threadIdx.x, l = tid & 63, lg = l >> 4, li = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, uniform by construction
+    const int rb = w % NRB, tg = w / NRB;                     // this wave's row block and tile group
 
     const int q0 = a.qsl[b];
     const int q_len = a.qsl[b + 1] - q0;
@@ -272,254 +288,303 @@ pd_partial_kernel(const PartialParams a) {
     };
 
     if (tb >= te) {  // no tiles: mark the split empty for the combine
-        for (int r = tid; r < R; r += kThreads) {
+        for (int r = tid; r < R; r += S::kThreadsWG) {
             a.part_m[prow(r)] = kNegInf;
             a.part_l[prow(r)] = 0.f;
         }
         return;
     }
 
-    // ---- per-lane query rows and Q^T operand (B of S^T = K Q^T) ----
-    bool rvalid[NRB];
-    int rpos[NRB];
-    half8_t qop[NRB][8];
-#pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) {
-        const int r = 16 * rb + li;
-        const int i = r / G, hh = r - (r / G) * G;
-        rvalid[rb] = r < R;
-        rpos[rb] = ctx0 + i;
-        const _Float16* qrow = a.q + (int64_t)(q0 + (rvalid[rb] ? i : 0)) * a.q_st + (int64_t)(g * G + hh) * kDim;
+    // ---- this wave's 16 query rows and their Q^T operand (B of S^T = K Q^T) ----
+    const int r = 16 * rb + li;
+    const bool rvalid = r < R;
+    const int qi = r / G, qh = r - (r / G) * G;
+    const int rpos = ctx0 + qi;
+    half8_t qop[8];
+    float qs = 0.f;  // sum of the row's 256 fp16 query values (64 per lane group)
+    {
+        const _Float16* qrow = a.q + (int64_t)(q0 + (rvalid ? qi : 0)) * a.q_st + (int64_t)(g * G + qh) * kDim;
 #pragma unroll
         for (int st = 0; st < 8; ++st) {
             half8_t v;
             const int dim = 64 * (st >> 1) + 16 * lg + 8 * (st & 1);
             __builtin_memcpy(&v, __builtin_assume_aligned(qrow + dim, 4), 16);
-            qop[rb][st] = rvalid[rb] ? v : (half8_t)(_Float16)0.0f;
+            qop[st] = rvalid ? v : (half8_t)(_Float16)0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qs += (float)qop[st][e];
         }
     }
+    const float qcorr = kWidenBias * xor_sum(xor_sum(qs, 16), 32);
 
-    float m_run[NRB], l_run[NRB];
-    float4_t oacc[NRB][17];
+    // Running state of the wave's rows: max (log2 units), this lane's partial sums of p and of
+    // the fp16 P' values (the latter removes the widening bias from O), and O^T.
+    float m_run = kNegInf, l_run = 0.f, cp_run = 0.f;
+    float4_t oacc[17];
 #pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) {
-        m_run[rb] = kNegInf;
-        l_run[rb] = 0.f;
-#pragma unroll
-        for (int m = 0; m < 17; ++m) oacc[rb][m] = (float4_t)0.f;
-    }
+    for (int m = 0; m < 17; ++m) oacc[m] = (float4_t)0.f;
 
     lds_u8* L = (lds_u8*)lds;
     const unsigned lds_base = (unsigned)(uintptr_t)L;
-    const unsigned wofs = (unsigned)(w * kWaveBytes);  // this wave's double buffer
-    // transposed-read lane address: lane pair (2r, 2r+1) of a 16-lane group names key slot r
+    const unsigned gofs = (unsigned)(tg * 2 * kTileBytes);  // this tile group's double buffer
+    // LDS offsets (inside a tile image) this lane reads, all fixed for the kernel:
+    //   K operand: key rows li and li + 16, bytes [16 lg, ...) of each 64-byte column group
+    const int k_ofs0 = row_ofs(li) + 16 * lg, k_ofs1 = row_ofs(li + 16) + 16 * lg;
+    //   transposed V reads: lane pair (2r, 2r+1) of a 16-lane group names key slot r
     const int slot = li >> 1;
     const int tkey = slot < 4 ? 4 * lg + slot : 16 + 4 * lg + (slot - 4);
-    const int tr_lane = 16 * tkey + 8 * (li & 1);
+    const int v_ofs = row_ofs(tkey) + 256 + 8 * (li & 1);
+    const int vt_ofs = kTailOfs + 16 * tkey + 8 * (li & 1);
+    //   scales of this lane's S^T keys 16u + 4lg + j: k_scale at row byte 256, v_scale in the tail
+    const int ks_ofs = row_ofs(4 * lg) + 256;
+    const int vs_ofs = kTailOfs + 16 * (4 * lg) + 12;
+    const unsigned voff_pair = (unsigned)((l >> 5) * a.k_ss) + 16u * (unsigned)(l & 31);
 
     // The block table is read-only for the kernel's lifetime: read it through the constant
-    // address space so uniform lookups become scalar loads (they must not share the vector
-    // memory counter with the K/V stream, or every lookup would drain the DMA pipeline).
+    // address space so uniform lookups become scalar loads.
     const_int_ptr bt_row = (const_int_ptr)(uintptr_t)(a.block_table + (int64_t)b * a.bt_stride);
+    PageTable pt;
+    pt.glob = bt_row;
+    {
+        const int pk_first = max(tb * kTile, lo), pk_last = min(te * kTile, hi) - 1;
+        pt.pfirst = pk_first / a.block_size;
+        const int npages = pk_last / a.block_size - pt.pfirst + 1;
+        pt.in_lds = npages <= kBtCache;
+        pt.lds = (const lds_int*)(L + S::kLdsBt);
+        if (pt.in_lds) {
+            lds_int* dst = (lds_int*)(L + S::kLdsBt);
+            for (int i = tid; i < npages; i += S::kThreadsWG)
+                dst[i] = a.block_table[(int64_t)b * a.bt_stride + pt.pfirst + i];
+        }
+        __syncthreads();
+    }
 
-    const int my_first = tb + w;
-    const int nt = my_first < te ? (te - 1 - my_first) / kWaves + 1 : 0;
-    const int rho = l & 31;
+    // tiles of this tile group: tb + tg + n * TG, n < nt_max (all waves run nt_max iterations
+    // so that they meet at the same barriers)
+    const int nt_max = (te - tb + TG - 1) / TG;
+    auto tile_of = [&](int n) { return tb + tg + n * TG; };
 
-    auto compute_tile = [&](int tile, unsigned kofs, unsigned vofs) {
-        // ---- S^T = K Q^T ----
-        float4_t sacc[NRB][2];
+    // ---- scores of one tile: S^T = K Q^T (two interleaved MFMA chains), times k_scale, minus
+    //      the widening bias; sv = -inf where masked; returns this lane's max ----
+    auto tile_scores = [&](int tile, const lds_u8* T, float (&sv)[8], bool& interior) __attribute__((always_inline)) {
+        uint4_t kraw[2][4];
 #pragma unroll
-        for (int rb = 0; rb < NRB; ++rb) sacc[rb][0] = sacc[rb][1] = (float4_t)0.f;
+        for (int c = 0; c < 4; ++c) {
+            kraw[0][c] = *(const lds_uint4*)(T + k_ofs0 + 64 * c);
+            kraw[1][c] = *(const lds_uint4*)(T + k_ofs1 + 64 * c);
+        }
+        float4_t sacc[2];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int c = 0; c < 4; ++c) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const uint4_t kraw = *(const lds_uint4*)(L + kofs + 512 * (4 * c + lg) + 16 * (li + 16 * u));
-                const half8_t k0 = widen_i8x8(kraw.x, kraw.y);
-                const half8_t k1 = widen_i8x8(kraw.z, kraw.w);
+            for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
-                for (int rb = 0; rb < NRB; ++rb) {
-                    sacc[rb][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qop[rb][2 * c], sacc[rb][u], 0, 0, 0);
-                    sacc[rb][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qop[rb][2 * c + 1], sacc[rb][u], 0, 0, 0);
+                for (int u = 0; u < 2; ++u) {
+                    const half8_t kf = hh == 0 ? widen_i8x8(kraw[u][c].x, kraw[u][c].y)
+                                               : widen_i8x8(kraw[u][c].z, kraw[u][c].w);
+                    sacc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qop[2 * c + hh],
+                                                                     (c | hh) ? sacc[u] : (float4_t)0.f, 0, 0, 0);
                 }
             }
         }
+        float ks[8];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                ks[4 * u + j] = *(const lds_float*)(T + ks_ofs + row_ofs(16 * u + j)) * a.scale_log2;
+        const int kb = tile * kTile;
+        // Interior tile: every key is visible to every row (padding rows have Q = 0 and are
+        // never written out), so no per-element mask is needed.
+        interior = kb >= lo && kb + kTile <= hi;
+        if (a.causal) interior = interior && kb + kTile - 1 <= ctx0;
+        if (a.window > 0) interior = interior && (ctx0 + ql - 1) - kb < a.window;
+        float mx = kNegInf;
+        if (interior) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                sv[e] = (sacc[e >> 2][e & 3] - qcorr) * ks[e];
+                mx = fmaxf(mx, sv[e]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int t = kb + 16 * (e >> 2) + 4 * lg + (e & 3);
+                const bool vis = rvalid & (t >= lo) & (t < hi) & (!a.causal | (t <= rpos)) &
+                                 ((a.window <= 0) | ((rpos - t) < a.window));
+                sv[e] = vis ? (sacc[e >> 2][e & 3] - qcorr) * ks[e] : kNegInf;
+                mx = fmaxf(mx, sv[e]);
+            }
+        }
+        return mx;
+    };
 
-        // ---- scales of this lane's 8 keys 16u + 4lg + j (k_scale at row byte 256, v_scale at 516) ----
-        float ks[2][4], vs[2][4];
+    // ---- P' = 2^(s - m) * v_scale * 16 (fp16), then O^T += V^T P'^T ----
+    auto tile_values = [&](const lds_u8* T, const float (&sv)[8], bool interior) __attribute__((always_inline)) {
+        float psum = 0.f, csum = 0.f;
+        _Float16 pv[8];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int key = 16 * u + 4 * lg + j;
-                ks[u][j] = *(const lds_float*)(L + vofs + 16 * key + (256 - kVFirst)) * a.scale_log2;
-                vs[u][j] = *(const lds_float*)(L + vofs + 512 * 16 + 16 * key + (516 - kVFirst - 256)) * kPScale;
+                const int e = 4 * u + j;
+                const float vsc = *(const lds_float*)(T + vs_ofs + 16 * (16 * u + j)) * kPScale;
+                // masked scores are -inf; the select also keeps a NaN scale of a masked row out
+                const bool vis = interior || sv[e] > kNegInf;
+                const float p = vis ? __builtin_amdgcn_exp2f(sv[e] - m_run) : 0.f;
+                psum += p;
+                pv[e] = (_Float16)(vis ? p * vsc : 0.f);
+                csum += (float)pv[e];
             }
         }
-
-        // ---- online softmax, P' ----
-        const int kb = tile * kTile;
-        // Interior tile: every key is visible to every row (padding rows have Q = 0 and
-        // are never written out), so no per-element mask is needed.
-        bool interior = kb >= lo && kb + kTile <= hi;
-        if (a.causal) interior = interior && kb + kTile - 1 <= ctx0;
-        if (a.window > 0) interior = interior && (ctx0 + ql - 1) - kb < a.window;
-        half8_t pop[NRB];
-#pragma unroll
-        for (int rb = 0; rb < NRB; ++rb) {
-            float sv[2][4];
-            bool vis[2][4];
-            float mloc = kNegInf;
-            if (interior) {
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        vis[u][j] = true;
-                        sv[u][j] = sacc[rb][u][j] * ks[u][j];
-                        mloc = fmaxf(mloc, sv[u][j]);
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int t = kb + 16 * u + 4 * lg + j;
-                        bool ok = rvalid[rb] && t >= lo && t < hi;
-                        if (a.causal) ok = ok && t <= rpos[rb];
-                        if (a.window > 0) ok = ok && (rpos[rb] - t) < a.window;
-                        vis[u][j] = ok;
-                        sv[u][j] = ok ? sacc[rb][u][j] * ks[u][j] : kNegInf;
-                        mloc = fmaxf(mloc, sv[u][j]);
-                    }
-                }
-            }
-            mloc = xor_max(mloc, 16);
-            mloc = xor_max(mloc, 32);
-            const bool raise = mloc > m_run[rb] + kLazy;
-            // wave-uniform; after the first tile it is rarely taken
-            const int any_raise = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_ballot_w64(raise) != 0);
-            {
-                const float m_new = raise ? mloc : m_run[rb];
-                const float alpha = m_run[rb] == kNegInf ? 0.f : __builtin_amdgcn_exp2f(m_run[rb] - m_new);
-                l_run[rb] *= alpha;
-                m_run[rb] = m_new;
-#pragma unroll
-                for (int m = 0; m < 17; ++m) scale_acc_if(oacc[rb][m], alpha, any_raise);
-            }
-            float psum = 0.f;
-            _Float16 pv[8];
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float p = vis[u][j] ? __builtin_amdgcn_exp2f(sv[u][j] - m_run[rb]) : 0.f;
-                    psum += p;
-                    pv[4 * u + j] = (_Float16)(vis[u][j] ? p * vs[u][j] : 0.f);
-                }
-            }
-            l_run[rb] += psum;
-            pop[rb] = half8_t{pv[0], pv[1], pv[2], pv[3], pv[4], pv[5], pv[6], pv[7]};
-        }
-
-        // ---- O^T += V^T P^T ----
+        l_run += psum;
+        cp_run += csum;
+        const half8_t pop = half8_t{pv[0], pv[1], pv[2], pv[3], pv[4], pv[5], pv[6], pv[7]};
 #pragma unroll
         for (int m = 0; m < 17; ++m) {
-            const int2_t raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_int2*)(L + vofs + 512 * m + tr_lane));
-            const half8_t vop = widen_i8x8((unsigned)raw.x, (unsigned)raw.y);
-#pragma unroll
-            for (int rb = 0; rb < NRB; ++rb)
-                oacc[rb][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop[rb], oacc[rb][m], 0, 0, 0);
+            const int ofs = m < 16 ? v_ofs + 16 * m : vt_ofs;
+            const int2_t raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_int2*)(T + ofs));
+            oacc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(widen_i8x8((unsigned)raw.x, (unsigned)raw.y), pop,
+                                                             oacc[m], 0, 0, 0);
         }
     };
 
-    if (nt > 0) {
-        TilePages pg = tile_pages<kFastBT>(a, bt_row, my_first, lo, hi);
-        issue_tile(tile_row<kFastBT>(a, bt_row, pg, rho, g), h, lds_base + wofs, lds_base + wofs + kKBytes);
-        if (nt > 1) pg = tile_pages<kFastBT>(a, bt_row, my_first + kWaves, lo, hi);
-        for (int n = 0; n < nt; ++n) {
-            const unsigned cur = wofs + (unsigned)((n & 1) * kTileBytes);
-            if (n + 1 < nt) {
-                const unsigned nxt = wofs + (unsigned)(((n + 1) & 1) * kTileBytes);
-                issue_tile(tile_row<kFastBT>(a, bt_row, pg, rho, g), h, lds_base + nxt, lds_base + nxt + kKBytes);
-                if (n + 2 < nt) pg = tile_pages<kFastBT>(a, bt_row, my_first + (n + 2) * kWaves, lo, hi);
-                wait_vm<kDmaPerTile>();
-            } else {
+    // Tile loop. Per iteration: wait for this wave's DMAs of the current tile, meet the other
+    // waves (the whole tile has landed, and every wave is done with the other buffer), issue this
+    // wave's share of the next tile's DMAs into that buffer, compute. The fast inner loop has no
+    // rescale: a row's running max is raised only when a tile's score exceeds it by more than
+    // kLazy (one ballot decides), and then the loop is left, the rows are rescaled with the
+    // cross-lane row max, the tile is finished and the loop resumes. This keeps the O
+    // accumulators in AGPRs, untouched by the vector ALU, on the common path.
+    auto tile_loop = [&](auto lds_flag) __attribute__((always_inline)) {
+        constexpr bool kLds = decltype(lds_flag)::value;
+        if (tile_of(0) < te)
+            issue_tile<kFastBT, kLds, NRB>(a, pt, tile_of(0), lo, hi, g, l, lds_base + gofs, voff_pair, rb);
+        int n = 0;
+        float sv[8];
+        bool interior = true;
+        const lds_u8* T = L;
+        while (n < nt_max) {
+            bool rare = false;
+            for (; n < nt_max; ++n) {
                 wait_vm<0>();
+                __syncthreads();
+                if (tile_of(n + 1) < te) {
+                    const unsigned nxt = gofs + (unsigned)(((n + 1) & 1) * kTileBytes);
+                    issue_tile<kFastBT, kLds, NRB>(a, pt, tile_of(n + 1), lo, hi, g, l, lds_base + nxt, voff_pair,
+                                                   rb);
+                }
+                if (tile_of(n) >= te) continue;
+                T = L + gofs + (n & 1) * kTileBytes;
+                const float mloc = tile_scores(tile_of(n), T, sv, interior);
+                if (__builtin_amdgcn_ballot_w64(mloc > m_run + kLazy) != 0) {
+                    rare = true;
+                    break;
+                }
+                tile_values(T, sv, interior);
             }
-            compute_tile(my_first + n * kWaves, cur, cur + kKBytes);
+            if (!rare) break;
+            // rare path: raise the running max of the rows that need it, rescale, finish the tile
+            float mloc = kNegInf;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mloc = fmaxf(mloc, sv[e]);
+            const float mrow = xor_max(xor_max(mloc, 16), 32);
+            const float m_new = mrow > m_run + kLazy ? mrow : m_run;
+            const float alpha = m_run == kNegInf ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_run *= alpha;
+            cp_run *= alpha;
+#pragma unroll
+            for (int m = 0; m < 17; ++m) oacc[m] *= alpha;
+            tile_values(T, sv, interior);
+            ++n;
         }
-    }
-    // ---- merge the 4 waves ----
-#pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) {
-        float lt = xor_sum(l_run[rb], 16);
-        l_run[rb] = xor_sum(lt, 32);
-    }
-    float* wm = reinterpret_cast<float*>(lds + kLdsStats);
-    float* wl = wm + kWaves * 16 * kMaxRowBlocks;
-    __syncthreads();  // every wave is done with its loop buffers (the merge buffer aliases them)
+    };
+    if (pt.in_lds)
+        tile_loop(std::true_type{});
+    else
+        tile_loop(std::false_type{});
+    wait_vm<0>();
+
+    // ---- merge the TG waves of each row block through LDS and write the partials ----
+    const float l_row = xor_sum(xor_sum(l_run, 16), 32);
+    const float corr = kWidenBias * xor_sum(xor_sum(cp_run, 16), 32);  // sum of the row's P'
+    float* wm = reinterpret_cast<float*>(lds + S::kLdsStats);           // [NRB][TG][16]
+    float* wl = wm + NRB * TG * 16;
+    __syncthreads();  // every wave is done with the tile buffers (the merge buffer aliases them)
     if (lg == 0) {
+        wm[(rb * TG + tg) * 16 + li] = m_run;
+        wl[(rb * TG + tg) * 16 + li] = l_row;
+    }
+    __syncthreads();
+    {
+        float M = kNegInf;
 #pragma unroll
-        for (int rb = 0; rb < NRB; ++rb) {
-            wm[w * 16 * kMaxRowBlocks + 16 * rb + li] = m_run[rb];
-            wl[w * 16 * kMaxRowBlocks + 16 * rb + li] = l_run[rb];
+        for (int t = 0; t < TG; ++t) M = fmaxf(M, wm[(rb * TG + t) * 16 + li]);
+        const float f = m_run == kNegInf ? 0.f : exp2f(m_run - M) * (1.0f / kPScale);
+        float* ob = reinterpret_cast<float*>(lds) + ((rb * TG + tg) * 16 + li) * kOPitch;
+#pragma unroll
+        for (int m = 0; m < 17; ++m) {
+            // block m < 16 covers dims 16m-4 .. 16m+11, block 16 dims 244..255 (only lg == 2 is new)
+            const int d0 = m < 16 ? 16 * m - 4 + 4 * lg : (lg == 2 ? 252 : -1);
+            if (d0 >= 0 && d0 < kDim) *reinterpret_cast<float4_t*>(ob + d0) = (oacc[m] - corr) * f;
         }
     }
     __syncthreads();
-    float* obuf = reinterpret_cast<float*>(lds);
+    {
+        // thread -> (row block, row, chunk of CH dims); sum the TG tile groups
+        constexpr int CH = 4096 / (S::kThreadsWG / NRB);
+        const int orb = tid / (S::kThreadsWG / NRB), idx = tid % (S::kThreadsWG / NRB);
+        const int orow = idx / (kDim / CH), dq = (idx % (kDim / CH)) * CH;
+        const int rr = 16 * orb + orow;
+        if (rr < R) {
+            float Mr = kNegInf;
 #pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) {
-        const int row = 16 * rb + li;
-        float M = kNegInf;
+            for (int t = 0; t < TG; ++t) Mr = fmaxf(Mr, wm[(orb * TG + t) * 16 + orow]);
+            float* dst = a.part_o + prow(rr) * kDim + dq;
 #pragma unroll
-        for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, wm[ww * 16 * kMaxRowBlocks + row]);
-        const float f = m_run[rb] == kNegInf ? 0.f : exp2f(m_run[rb] - M) * (1.0f / kPScale);
-        float* ob = obuf + (w * 16 + li) * kOPitch;
+            for (int q4 = 0; q4 < CH / 4; ++q4) {
+                float4_t acc = (float4_t)0.f;
 #pragma unroll
-        for (int m = 0; m < 17; ++m) {
-            const int d0 = 16 * m - (260 - kVFirst) + 4 * lg;  // block m covers dims 16m-12 .. 16m+3
-            if (d0 >= 0 && d0 < kDim) *reinterpret_cast<float4_t*>(ob + d0) = oacc[rb][m] * f;
-        }
-        __syncthreads();
-        {
-            const int orow = tid >> 4, dq = (tid & 15) * 16;
-            const int r = 16 * rb + orow;
-            if (r < R) {
-                float Mr = kNegInf;
+                for (int t = 0; t < TG; ++t)
+                    acc += *reinterpret_cast<const float4_t*>(reinterpret_cast<const float*>(lds) +
+                                                              ((orb * TG + t) * 16 + orow) * kOPitch + dq + 4 * q4);
+                *reinterpret_cast<float4_t*>(dst + 4 * q4) = acc;
+            }
+            if (dq == 0) {
+                float Lr = 0.f;
 #pragma unroll
-                for (int ww = 0; ww < kWaves; ++ww) Mr = fmaxf(Mr, wm[ww * 16 * kMaxRowBlocks + r]);
-                float* dst = a.part_o + prow(r) * kDim + dq;
-#pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4) {
-                    float4_t acc = (float4_t)0.f;
-#pragma unroll
-                    for (int ww = 0; ww < kWaves; ++ww)
-                        acc += *reinterpret_cast<const float4_t*>(obuf + (ww * 16 + orow) * kOPitch + dq + 4 * q4);
-                    *reinterpret_cast<float4_t*>(dst + 4 * q4) = acc;
+                for (int t = 0; t < TG; ++t) {
+                    const float mw = wm[(orb * TG + t) * 16 + orow];
+                    if (mw != kNegInf) Lr += exp2f(mw - Mr) * wl[(orb * TG + t) * 16 + orow];
                 }
-                if ((tid & 15) == 0) {
-                    float L = 0.f;
-#pragma unroll
-                    for (int ww = 0; ww < kWaves; ++ww) {
-                        const float mw = wm[ww * 16 * kMaxRowBlocks + r];
-                        if (mw != kNegInf) L += exp2f(mw - Mr) * wl[ww * 16 * kMaxRowBlocks + r];
-                    }
-                    a.part_m[prow(r)] = Mr;
-                    a.part_l[prow(r)] = L;
-                }
+                a.part_m[prow(rr)] = Mr;
+                a.part_l[prow(rr)] = Lr;
             }
         }
-        __syncthreads();
     }
 }
 
-// One workgroup per (token, q head): 4 groups of 64 threads split the partials, each thread
-// owns 4 output dims; the groups are merged through LDS. Follows pth_dec.cu:245-283.
+// One workgroup per (token, q head), semantics of pth_dec.cu:245-283: M = max_p m_p,
+// L = sum_p 2^(m_p - M) l_p, out = sum_p 2^(m_p - M) O_p / L (0 if L = 0). The weights are
+// computed once per 256 splits into LDS; then 4 groups of 64 threads (4 output dims each)
+// stream a quarter of the partials with independent loads, and the groups are summed through
+// LDS. Splits marked empty (m = -inf) contribute through a select, so stale partial memory
+// from an earlier call can never leak in.
+__device__ __forceinline__ float wave_max64(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum64(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
 __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) {
-    __shared__ float sm_acc[4][64][5];
+    __shared__ float s_w[256];
+    __shared__ float s_red[8];
+    __shared__ float4_t s_acc[3][64];
     const int tok = blockIdx.x, head = blockIdx.y, Hq = gridDim.y;
     const int tid = threadIdx.x, d4 = tid & 63, grp = tid >> 6;
     int b = 0;
@@ -528,33 +593,51 @@ __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) 
     if (a.seq_lens[b] <= 0) return;
     if (tok - a.qsl[b] >= a.qmax) return;  // rows past qmax are not computed
     const int64_t base = ((int64_t)tok * Hq + head) * a.nseg;
-    float M = kNegInf;
-    for (int p = 0; p < a.nsplit; ++p) M = fmaxf(M, a.part_m[base + p]);
-    float L = 0.f;
+
+    float mx = kNegInf;
+    for (int p = tid; p < a.nsplit; p += 256) mx = fmaxf(mx, a.part_m[base + p]);
+    mx = wave_max64(mx);
+    if (d4 == 0) s_red[grp] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+
+    float lsum = 0.f;
     float4_t acc = (float4_t)0.f;
-    if (M != kNegInf) {
-        for (int p = 0; p < a.nsplit; ++p) {
+    for (int c0 = 0; c0 < a.nsplit; c0 += 256) {
+        const int p = c0 + tid;
+        float w = 0.f;
+        if (p < a.nsplit) {
             const float mp = a.part_m[base + p];
-            if (mp == kNegInf) continue;
-            const float wgt = exp2f(mp - M);
-            L += wgt * a.part_l[base + p];
-            if ((p & 3) == grp)
-                acc += wgt * reinterpret_cast<const float4_t*>(a.part_o + (base + p) * kDim)[d4];
+            if (mp != kNegInf) {
+                w = exp2f(mp - M);
+                lsum += w * a.part_l[base + p];
+            }
         }
+        s_w[tid] = w;
+        __syncthreads();
+        const int n = min(256, a.nsplit - c0);
+        const float4_t* po = reinterpret_cast<const float4_t*>(a.part_o + (base + c0) * kDim) + d4;
+#pragma unroll 8
+        for (int j = grp; j < n; j += 4) {
+            const float wj = s_w[j];
+            const float4_t o = po[(int64_t)j * (kDim / 4)];
+            acc += wj != 0.f ? wj * o : (float4_t)0.f;
+        }
+        __syncthreads();
     }
-    sm_acc[grp][d4][0] = acc.x;
-    sm_acc[grp][d4][1] = acc.y;
-    sm_acc[grp][d4][2] = acc.z;
-    sm_acc[grp][d4][3] = acc.w;
+    lsum = wave_sum64(lsum);
+    if (d4 == 0) s_red[4 + grp] = lsum;
+    if (grp > 0) s_acc[grp - 1][d4] = acc;
     __syncthreads();
     if (grp == 0) {
+        acc += s_acc[0][d4] + s_acc[1][d4] + s_acc[2][d4];
+        const float L = s_red[4] + s_red[5] + s_red[6] + s_red[7];
         const float inv = L > 0.f ? 1.f / L : 0.f;
+        typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+        const half4_t h = {(_Float16)(acc.x * inv), (_Float16)(acc.y * inv), (_Float16)(acc.z * inv),
+                           (_Float16)(acc.w * inv)};
         _Float16* o = a.out + (int64_t)tok * a.o_st + (int64_t)head * a.o_sh + 4 * d4;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float v = sm_acc[0][d4][j] + sm_acc[1][d4][j] + sm_acc[2][d4][j] + sm_acc[3][d4][j];
-            o[j] = (_Float16)(v * inv);
-        }
+        __builtin_memcpy(o, &h, 8);
     }
 }
 
@@ -582,7 +665,7 @@ struct LaunchArgs {
     int window, causal;
 };
 
-bool fast_block_table(int bs) { return bs == 16 || bs >= 32; }
+bool fast_block_table(int bs) { return bs == 16 || (bs >= 32 && bs % 2 == 0); }
 
 hipError_t check_args(const LaunchArgs& x, bool strict_reference) {
     if (x.heads_kv < 1 || x.heads_q < 1 || x.heads_q % x.heads_kv != 0) return hipErrorInvalidValue;
@@ -600,10 +683,11 @@ hipError_t check_args(const LaunchArgs& x, bool strict_reference) {
 
 template <int NRB>
 hipError_t launch_partial_nrb(const PartialParams& p, dim3 grid, hipStream_t stream, bool fast) {
+    const dim3 block(Shape<NRB>::kThreadsWG);
     if (fast)
-        hipLaunchKernelGGL((pd_partial_kernel<NRB, true>), grid, dim3(kThreads), 0, stream, p);
+        hipLaunchKernelGGL((pd_partial_kernel<NRB, true>), grid, block, 0, stream, p);
     else
-        hipLaunchKernelGGL((pd_partial_kernel<NRB, false>), grid, dim3(kThreads), 0, stream, p);
+        hipLaunchKernelGGL((pd_partial_kernel<NRB, false>), grid, block, 0, stream, p);
     return hipGetLastError();
 }
 
