@@ -31,6 +31,58 @@ sys.path.insert(0, ROOT)
 METRIC = "µs/layer + achieved KV GB/s (% of HBM peak), MTP 24-row decode at 61k ctx"
 HBM_PEAK_GBS = 8000.0
 NSEG = 128
+CALIB_BYTES = 256 << 20
+CALIB_COPIES = 8
+
+
+def _pmc_dispatches(run_dir, counter):
+    """{dispatch id: (kernel name, summed counter value)} from a rocprofv3 --pmc csv run directory."""
+    import csv
+    import glob
+
+    files = glob.glob(os.path.join(run_dir, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {run_dir}")
+    out = {}
+    for fn in files:
+        with open(fn) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] != counter:
+                    continue
+                key = (fn, int(r["Dispatch_Id"]))
+                name, v = out.get(key, (r["Kernel_Name"], 0.0))
+                out[key] = (name, v + float(r["Counter_Value"]))
+    return out
+
+
+def summarize_traffic(args):
+    """HBM bytes per pd_partial_kernel launch from FETCH_SIZE and WRITE_SIZE runs of --profile-only.
+
+    Both counters are read in KiB per dispatch. Each is scaled by what it reads for the calibration
+    copy (CALIB_BYTES read and CALIB_BYTES written per launch, the last CALIB_COPIES dispatches)."""
+    res = {}
+    for counter, run_dir in (("FETCH_SIZE", args.traffic_summary[0]), ("WRITE_SIZE", args.traffic_summary[1])):
+        d = _pmc_dispatches(run_dir, counter)
+        order = sorted(d)
+        part = [d[k][1] for k in order if "pd_partial_kernel" in d[k][0]]
+        other = [d[k][1] for k in order if not d[k][0].startswith("pd_")]
+        calib = other[-CALIB_COPIES:]
+        if not part or len(calib) < CALIB_COPIES:
+            raise SystemExit(f"{counter}: {len(part)} partial dispatches, {len(calib)} calibration copies")
+        part.sort()
+        calib.sort()
+        p_kib, c_kib = part[len(part) // 2], calib[len(calib) // 2]
+        factor = (CALIB_BYTES / 1024.0) / c_kib
+        res[counter] = {"partial_kib_median": p_kib, "calib_copy_kib_median": c_kib, "calib_factor": factor,
+                        "partial_bytes": p_kib * 1024.0 * factor, "dispatches": len(part)}
+    total = res["FETCH_SIZE"]["partial_bytes"] + res["WRITE_SIZE"]["partial_bytes"]
+    summary = {"kernel": "pd_partial_kernel", "workload": "MTP verify 4 x 24/4 heads, ctx 61440+4, bs 16",
+               "nsplit": args.nsplit, "hbm_bytes_per_launch": round(total), "counters": res,
+               "calibration": f"{CALIB_COPIES} copies of {CALIB_BYTES} bytes (read + write) after the partial "
+                              f"launches; factor = known bytes / counter bytes"}
+    with open(args.traffic_out, "w") as f:
+        json.dump(summary, f, indent=1)
+    print(json.dumps(summary))
 
 
 def load_package():
@@ -86,8 +138,19 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=5)
     ap.add_argument("--profile-only", action="store_true",
-                    help="run the timed loop of the partial kernel only (for rocprofv3 counter runs)")
+                    help="replay the partial kernel only, then a plain copy of known size that calibrates the "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters (for counter runs)")
+    ap.add_argument("--hot", action="store_true",
+                    help="also time every call on the same (Infinity-Cache resident) cache; reported beside")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="no GPU work: turn two rocprofv3 --pmc runs of --profile-only (FETCH_SIZE, WRITE_SIZE) "
+                         "into HBM bytes per partial launch, written to --traffic-out")
+    ap.add_argument("--traffic-out", default=os.path.join(ROOT, "profiles", "pd_partial_mtp61k_traffic.json"))
     args = ap.parse_args()
+
+    if args.traffic_summary:
+        summarize_traffic(args)
+        return
 
     if args.gpus != 1:
         print(json.dumps({"error": f"--gpus {args.gpus}: this benchmark measures one GPU; the operator is "
@@ -150,7 +213,15 @@ def main():
         for _ in range(max(1, args.steps // R)):
             g_part.replay()
         torch.cuda.synchronize()
-        print(json.dumps({"profile_only": True, "partial_launches": R * max(1, args.steps // R)}))
+        # calibration: CALIB_COPIES plain device copies of CALIB_BYTES each, launched last
+        src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(CALIB_COPIES):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_only": True, "partial_launches": R * max(1, args.steps // R),
+                          "nsplit": args.nsplit, "calib_copies": CALIB_COPIES, "calib_bytes": CALIB_BYTES}))
         return
 
     warm_reps = max(1, math.ceil(args.warmup / R))
@@ -163,15 +234,17 @@ def main():
         for _ in range(warm_reps):
             g_part.replay()
         part_ms = time_graph(torch, g_part, reps, stream) / R         # partial kernel per launch
-    # same cache every call (Infinity-Cache resident): reported beside, never as `value`
-    g_hot = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g_hot, stream=stream):
-        for _ in range(R):
-            op(caches[0])
-    with torch.cuda.stream(stream):
-        for _ in range(warm_reps):
-            g_hot.replay()
-        ms_hot = time_graph(torch, g_hot, reps, stream) / R
+    ms_hot = None
+    if args.hot:
+        # same cache every call (Infinity-Cache resident): reported beside, never as `value`
+        g_hot = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_hot, stream=stream):
+            for _ in range(R):
+                op(caches[0])
+        with torch.cuda.stream(stream):
+            for _ in range(warm_reps):
+                g_hot.replay()
+            ms_hot = time_graph(torch, g_hot, reps, stream) / R
 
     us_layer = ms_rot * 1e3
     gbs = alg_bytes / (ms_rot * 1e-3) / 1e9
@@ -237,7 +310,7 @@ def main():
                      "frac": round(part_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "pd_partial_kernel", "avg_launch_us": round(part_ms * 1e3, 3),
                      "bytes_per_launch": partial_bytes},
-        "hot_cache_us_per_layer": round(ms_hot * 1e3, 3),
+        "hot_cache_us_per_layer": None if ms_hot is None else round(ms_hot * 1e3, 3),
         "tflops": round(flops / (ms_rot * 1e-3) / 1e12, 2),
         "cpu_baseline": cpu,
     }

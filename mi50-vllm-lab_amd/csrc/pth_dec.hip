@@ -564,79 +564,101 @@ pd_partial_kernel(const PartialParams a) {
     }
 }
 
-// One workgroup per (token, q head), semantics of pth_dec.cu:245-283: M = max_p m_p,
-// L = sum_p 2^(m_p - M) l_p, out = sum_p 2^(m_p - M) O_p / L (0 if L = 0). The weights are
-// computed once per 256 splits into LDS; then 4 groups of 64 threads (4 output dims each)
-// stream a quarter of the partials with independent loads, and the groups are summed through
-// LDS. Splits marked empty (m = -inf) contribute through a select, so stale partial memory
-// from an earlier call can never leak in.
 __device__ __forceinline__ float wave_max64(float v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
 }
-__device__ __forceinline__ float wave_sum64(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
+
+// Log-sum-exp merge of the split partials (pth_dec.cu:245-283 semantics): M = max_p m_p,
+// L = sum_p 2^(m_p - M) l_p, out = sum_p 2^(m_p - M) O_p / L, and 0 when L == 0. Grid
+// (num_tokens, heads_q, 4): each workgroup merges one 64-dim quarter of one (token, head) row.
+// Thread (sg = tid / 16, c = tid % 16) owns float4 column c of segments sg, sg + 16, ...; all
+// partial loads of the first 16 * kCombPer segments are issued before the one barrier that
+// publishes M, so the merge costs one memory round trip.
+constexpr int kCombPer = 8;
 
 __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) {
-    __shared__ float s_w[256];
-    __shared__ float s_red[8];
-    __shared__ float4_t s_acc[3][64];
-    const int tok = blockIdx.x, head = blockIdx.y, Hq = gridDim.y;
-    const int tid = threadIdx.x, d4 = tid & 63, grp = tid >> 6;
+    __shared__ float s_red[4];
+    __shared__ float s_l[4];
+    __shared__ float4_t s_acc[4][16];
+    const int tok = blockIdx.x, head = blockIdx.y, quarter = blockIdx.z, Hq = gridDim.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = tid & 15, sg = tid >> 4;
+
+    // sequence of this token = number of sequences whose query rows end at or before it
     int b = 0;
-    while (b < a.num_seqs && a.qsl[b + 1] <= tok) ++b;
+    for (int i0 = 0; i0 < a.num_seqs; i0 += 64) {
+        const int i = i0 + lane + 1;
+        const bool ended = i <= a.num_seqs && a.qsl[i] <= tok;
+        b += __popcll(__ballot(ended));
+    }
     if (b >= a.num_seqs || tok < a.qsl[b]) return;  // padding token
     if (a.seq_lens[b] <= 0) return;
     if (tok - a.qsl[b] >= a.qmax) return;  // rows past qmax are not computed
-    const int64_t base = ((int64_t)tok * Hq + head) * a.nseg;
 
+    const int64_t base = ((int64_t)tok * Hq + head) * a.nseg;
+    const float* pm = a.part_m + base;
+    const float* pl = a.part_l + base;
+    const float4_t* po = reinterpret_cast<const float4_t*>(a.part_o + base * kDim + quarter * 64) + c;
+
+    float mv[kCombPer], lv[kCombPer];
+    float4_t ov[kCombPer];
+#pragma unroll
+    for (int i = 0; i < kCombPer; ++i) {
+        const int sgi = sg + 16 * i;
+        const bool ok = sgi < a.nsplit;
+        mv[i] = ok ? pm[sgi] : kNegInf;
+        lv[i] = ok ? pl[sgi] : 0.f;
+        ov[i] = ok ? po[(int64_t)sgi * (kDim / 4)] : (float4_t)0.f;
+    }
     float mx = kNegInf;
-    for (int p = tid; p < a.nsplit; p += 256) mx = fmaxf(mx, a.part_m[base + p]);
+#pragma unroll
+    for (int i = 0; i < kCombPer; ++i) mx = fmaxf(mx, mv[i]);
+    for (int p = tid + 16 * kCombPer; p < a.nsplit; p += 256) mx = fmaxf(mx, pm[p]);
     mx = wave_max64(mx);
-    if (d4 == 0) s_red[grp] = mx;
+    if (lane == 0) s_red[wave] = mx;
     __syncthreads();
     const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
 
     float lsum = 0.f;
     float4_t acc = (float4_t)0.f;
-    for (int c0 = 0; c0 < a.nsplit; c0 += 256) {
-        const int p = c0 + tid;
-        float w = 0.f;
-        if (p < a.nsplit) {
-            const float mp = a.part_m[base + p];
-            if (mp != kNegInf) {
-                w = exp2f(mp - M);
-                lsum += w * a.part_l[base + p];
+    if (M != kNegInf) {
+#pragma unroll
+        for (int i = 0; i < kCombPer; ++i) {
+            const float w = mv[i] != kNegInf ? exp2f(mv[i] - M) : 0.f;
+            lsum += w * lv[i];
+            acc += w != 0.f ? w * ov[i] : (float4_t)0.f;  // empty splits leave part_o unwritten
+        }
+        for (int p = sg + 16 * kCombPer; p < a.nsplit; p += 16) {
+            const float mp = pm[p];
+            const float w = mp != kNegInf ? exp2f(mp - M) : 0.f;
+            if (w != 0.f) {
+                lsum += w * pl[p];
+                acc += w * po[(int64_t)p * (kDim / 4)];
             }
         }
-        s_w[tid] = w;
-        __syncthreads();
-        const int n = min(256, a.nsplit - c0);
-        const float4_t* po = reinterpret_cast<const float4_t*>(a.part_o + (base + c0) * kDim) + d4;
-#pragma unroll 8
-        for (int j = grp; j < n; j += 4) {
-            const float wj = s_w[j];
-            const float4_t o = po[(int64_t)j * (kDim / 4)];
-            acc += wj != 0.f ? wj * o : (float4_t)0.f;
-        }
-        __syncthreads();
     }
-    lsum = wave_sum64(lsum);
-    if (d4 == 0) s_red[4 + grp] = lsum;
-    if (grp > 0) s_acc[grp - 1][d4] = acc;
+    // reduce over the 16 segment slots: xor 16 / 32 inside the wave, then across the 4 waves
+#pragma unroll
+    for (int o = 16; o <= 32; o <<= 1) {
+        lsum += __shfl_xor(lsum, o, 64);
+        acc.x += __shfl_xor(acc.x, o, 64);
+        acc.y += __shfl_xor(acc.y, o, 64);
+        acc.z += __shfl_xor(acc.z, o, 64);
+        acc.w += __shfl_xor(acc.w, o, 64);
+    }
+    if (lane < 16) s_acc[wave][lane] = acc;
+    if (lane == 0) s_l[wave] = lsum;
     __syncthreads();
-    if (grp == 0) {
-        acc += s_acc[0][d4] + s_acc[1][d4] + s_acc[2][d4];
-        const float L = s_red[4] + s_red[5] + s_red[6] + s_red[7];
+    if (tid < 16) {
+        const float4_t r = s_acc[0][tid] + s_acc[1][tid] + s_acc[2][tid] + s_acc[3][tid];
+        const float L = s_l[0] + s_l[1] + s_l[2] + s_l[3];
         const float inv = L > 0.f ? 1.f / L : 0.f;
         typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-        const half4_t h = {(_Float16)(acc.x * inv), (_Float16)(acc.y * inv), (_Float16)(acc.z * inv),
-                           (_Float16)(acc.w * inv)};
-        _Float16* o = a.out + (int64_t)tok * a.o_st + (int64_t)head * a.o_sh + 4 * d4;
+        const half4_t h = {(_Float16)(r.x * inv), (_Float16)(r.y * inv), (_Float16)(r.z * inv),
+                           (_Float16)(r.w * inv)};
+        _Float16* o = a.out + (int64_t)tok * a.o_st + (int64_t)head * a.o_sh + quarter * 64 + 4 * tid;
         __builtin_memcpy(o, &h, 8);
     }
 }
@@ -737,7 +759,7 @@ hipError_t launch_combine(const LaunchArgs& x, hipStream_t stream) {
     c.nseg = x.nseg;
     c.nsplit = x.nsplit;
     c.qmax = x.qmax;
-    hipLaunchKernelGGL(pd_combine_kernel, dim3(x.num_tokens, x.heads_q), dim3(256), 0, stream, c);
+    hipLaunchKernelGGL(pd_combine_kernel, dim3(x.num_tokens, x.heads_q, 4), dim3(256), 0, stream, c);
     return hipGetLastError();
 }
 
