@@ -1,0 +1,165 @@
+"""Host-side behaviour of libpthdec.so that needs no GPU.
+
+The library loads, exports every entry point include/pth_dec.h declares, recognises the int8
+per-token-head cache layout like supported_layout (kernels/pth_dec/pth_dec.cpp:16-41), rejects
+bad arguments with the reference's messages (pth_dec.cpp:54-80) and error codes
+(hipErrorInvalidValue, pth_dec.cu:291-306), and treats an empty batch as a no-op. None of these
+calls reaches a device: every case here fails validation or has no tokens.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import mi50_vllm_lab_amd.kvcache as kvc
+from mi50_vllm_lab_amd import pth_dec
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "pth_dec.h")
+HIP_ERROR_INVALID_VALUE = 1
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return pth_dec.load_library()
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(pth_dec_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_symbols_exported(lib):
+    names = declared_functions()
+    assert names == sorted(pth_dec.EXPORTED_SYMBOLS)
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_version(lib):
+    assert pth_dec.version().startswith("pth_dec-gfx950")
+
+
+def make(layout="HND", **kw):
+    args = dict(ctxs=[40, 9], qlens=[4, 1], num_q_heads=12, num_kv_heads=2, block_size=16, layout=layout, seed=7)
+    args.update(kw)
+    return kvc.make_case(**args)
+
+
+@pytest.mark.parametrize("layout", ["HND", "NHD"])
+def test_supported_layout_accepts_cache_views(layout):
+    c = make(layout).cache
+    assert pth_dec.supported_layout(c.key_cache, c.value_cache, c.k_scale, c.v_scale)
+
+
+def test_supported_layout_rejects():
+    c = make().cache
+    kc, vc, ks, vs = c.key_cache, c.value_cache, c.k_scale, c.v_scale
+    assert not pth_dec.supported_layout(kc, kc, ks, vs)                       # V not at +260 B
+    assert not pth_dec.supported_layout(kc, vc, vs, vs)                       # k_scale not at +256 B
+    assert not pth_dec.supported_layout(kc, vc, ks, ks)                       # v_scale not at +516 B
+    assert not pth_dec.supported_layout(kc.view(torch.uint8), vc, ks, vs)     # dtype
+    assert not pth_dec.supported_layout(kc[..., :256], vc, ks, vs)            # row is not 260 wide
+    other = kvc.allocate_cache(c.num_blocks, c.block_size, c.num_kv_heads)   # unrelated storage
+    assert not pth_dec.supported_layout(kc, other.value_cache, ks, vs)
+
+
+def call_decode(lib, case, *, q=None, out=None, bt=None, part=None, num_seqs=None, qmax=None, nsplit=4,
+                key_cache=None):
+    q = case.q if q is None else q
+    T, hq = q.shape[0], q.shape[1]
+    out = torch.empty((T, hq, 256), dtype=torch.float16) if out is None else out
+    po, pm, pl = kvc.partial_buffers(max(T, 1), hq, 8, "cpu") if part is None else part
+    c = case.cache
+    tensors = (q, c.key_cache if key_cache is None else key_cache, c.value_cache, c.k_scale, c.v_scale,
+               case.block_table if bt is None else bt, case.seq_lens, case.query_start_loc, out)
+    descs = [pth_dec.describe(t) for t in tensors]
+    pdescs = [pth_dec.describe(t) for t in (po, pm, pl)]
+    err = ctypes.create_string_buffer(256)
+    rc = lib.pth_dec_decode(*[ctypes.byref(x) for x in descs], case.scale, *[ctypes.byref(x) for x in pdescs],
+                            case.num_seqs if num_seqs is None else num_seqs, case.qmax if qmax is None else qmax,
+                            nsplit, -1, 1, None, err, len(err))
+    return rc, err.value.decode()
+
+
+def test_decode_validation_messages(lib):
+    case = make()
+    T, hq = case.q.shape[0], case.q.shape[1]
+    cases = [
+        (dict(q=case.q.float()), "q must be fp16"),
+        (dict(q=case.q[..., :128]), "q must be fp16"),
+        (dict(out=torch.empty((T, hq, 128), dtype=torch.float16)), "out must be fp16"),
+        (dict(out=torch.empty((T, hq, 256), dtype=torch.float32)), "out must be fp16"),
+        (dict(key_cache=case.cache.value_cache), "KV cache views"),
+        (dict(bt=case.block_table.long()), "must be int32"),
+        (dict(part=(torch.empty((T, hq, 256, 8)).transpose(2, 3), torch.empty((T, hq, 8)),
+                    torch.empty((T, hq, 8)))), "partial buffers must be contiguous fp32"),
+        (dict(part=kvc.partial_buffers(max(T - 1, 1), hq, 8, "cpu")), "partial buffers too small"),
+        (dict(qmax=9), "qmax * (Hq / Hkv)"),
+        (dict(qmax=0), "qmax * (Hq / Hkv)"),
+        (dict(nsplit=9), "nsplit must be in [1, NSEG]"),
+        (dict(nsplit=0), "nsplit must be in [1, NSEG]"),
+        (dict(num_seqs=3), "per-sequence tensors too small"),
+    ]
+    for kw, msg in cases:
+        rc, text = call_decode(lib, case, **kw)
+        assert rc == 1 and msg in text, (kw.keys(), rc, text)
+    q5 = torch.zeros((T, 10, 256), dtype=torch.float16)  # 10 q heads over 2 kv heads: fine; 9 is not
+    rc, text = call_decode(lib, case, q=torch.zeros((T, 9, 256), dtype=torch.float16),
+                           out=torch.empty((T, 9, 256), dtype=torch.float16),
+                           part=kvc.partial_buffers(T, 9, 8, "cpu"))
+    assert rc == 1 and "multiple of heads_kv" in text
+    del q5
+
+
+def test_decode_empty_batch_is_noop(lib):
+    case = make()
+    q0 = case.q[:0]
+    rc, text = call_decode(lib, case, q=q0, out=torch.empty((0, 12, 256), dtype=torch.float16))
+    assert rc == 0, text
+
+
+def raw_launch(lib, fn, *, heads_q=24, heads_kv=4, qmax=4, nseg=8, nsplit=4, tokens=0, extra=()):
+    null_i = ctypes.POINTER(ctypes.c_int)()
+    null_f = ctypes.POINTER(ctypes.c_float)()
+    return fn(None, 6144, None, 0, 0, 0, null_i, 0, null_i, null_i, 1, tokens, heads_q, heads_kv, 16, 0.0625, qmax,
+              null_f, null_f, null_f, nseg, nsplit, None, 0, 0, None, *extra)
+
+
+def test_reference_launch_error_codes(lib):
+    f = lib.pth_dec_launch
+    assert raw_launch(lib, f) == 0                                    # no tokens: nothing launched
+    assert raw_launch(lib, f, heads_q=20) == HIP_ERROR_INVALID_VALUE  # G = 5 (reference supports 6 only)
+    assert raw_launch(lib, f, qmax=5) == HIP_ERROR_INVALID_VALUE      # reference qmax <= 4
+    assert raw_launch(lib, f, nsplit=9) == HIP_ERROR_INVALID_VALUE    # nsplit > NSEG
+    assert raw_launch(lib, f, nsplit=0) == HIP_ERROR_INVALID_VALUE
+    assert raw_launch(lib, f, heads_q=25) == HIP_ERROR_INVALID_VALUE  # not a multiple of heads_kv
+
+
+def test_window_launch_error_codes(lib):
+    f = lib.pth_dec_launch_window
+    assert raw_launch(lib, f, qmax=8, extra=(2048, 0)) == 0            # DFlash rows: 8 x 6 = 48
+    assert raw_launch(lib, f, qmax=9, extra=(2048, 0)) == HIP_ERROR_INVALID_VALUE
+    assert raw_launch(lib, f, heads_q=20, qmax=4, extra=(-1, 1)) == 0  # other G values are accepted
+
+
+def test_combine_launch_error_codes(lib):
+    null_i = ctypes.POINTER(ctypes.c_int)()
+    null_f = ctypes.POINTER(ctypes.c_float)()
+    f = lib.pth_dec_launch_combine
+    assert f(null_i, null_i, 1, 0, 24, 4, null_f, null_f, null_f, 8, 4, None, 0, 0, None) == 0
+    assert f(null_i, null_i, 1, 0, 24, 4, null_f, null_f, null_f, 8, 9, None, 0, 0, None) == HIP_ERROR_INVALID_VALUE
+    assert f(null_i, null_i, 0, 0, 24, 4, null_f, null_f, null_f, 8, 4, None, 0, 0, None) == HIP_ERROR_INVALID_VALUE
+
+
+def test_python_decode_refuses_host_tensors():
+    case = make()
+    po, pm, pl = kvc.partial_buffers(case.num_tokens, 12, 8, "cpu")
+    c = case.cache
+    with pytest.raises(RuntimeError):
+        pth_dec.decode(case.q, c.key_cache, c.value_cache, c.k_scale, c.v_scale, case.block_table, case.seq_lens,
+                       case.query_start_loc, torch.empty_like(case.q), case.scale, po, pm, pl, case.num_seqs,
+                       case.qmax, 4)
