@@ -64,6 +64,9 @@ typedef __attribute__((address_space(3))) int2_t lds_int2;
 typedef __attribute__((address_space(3))) uint4_t lds_uint4;
 typedef __attribute__((address_space(3))) float lds_float;
 typedef __attribute__((address_space(3))) int lds_int;
+typedef __attribute__((address_space(3))) uint64_t lds_u64;
+typedef unsigned long long ull2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) ull2_t lds_ull2;
 typedef const __attribute__((address_space(4))) int* const_int_ptr;  // scalar-cache loads
 
 constexpr int kDim = 256;             // head dim (the only one the cache row layout allows)
@@ -76,16 +79,22 @@ constexpr float kNegInf = -__builtin_inff();
 constexpr float kLazy = 4.0f;
 constexpr float kPScale = 16.0f;
 
-// LDS image of one tile: 16 blocks of two rows (2i, 2i+1) kPair bytes apart, row r's bytes
-// [0, 512) at row_ofs(r) (the 16-byte gap between blocks spreads the LDS banks), then the
-// tail block: row r's bytes [504, 520) at kTailOfs + 16 r (lanes 32-63 land a copy behind).
-constexpr int kPair = 1040;
-constexpr int kTailOfs = 16 * kPair;
-constexpr int kTileBytes = kTailOfs + 1024;
-constexpr int kOPitch = kDim + 4;     // floats per row of the merge buffer
-constexpr int kBtCache = 1024;        // block-table entries of a split kept in LDS
+// Per-wave LDS image of the V half of one tile. Chunk j (0..15) holds bytes
+// [256 + 16 j, 272 + 16 j) of the tile's 32 rows (chunk 0 starts with the row's k_scale), chunk
+// 16 holds bytes [504, 520) with the v_scale word cleared. Row r of a chunk sits at vrow(r)
+// (16 r, +128 for r >= 16), so the 8 rows one 16-lane group reads with ds_read_b64_tr_b8 cover
+// 32 distinct banks and a half-wave all 64.
+constexpr int kVChunks = 17;
+constexpr int kVPitch = 640;                       // bytes per chunk
+constexpr int kVImage = kVChunks * kVPitch;
+constexpr int kScalesOfs = kVImage;                // k_scale[32], then v_scale[32] (f32)
+constexpr int kWaveLds = kVImage + 2 * kTile * 4;  // LDS bytes per wave
+constexpr int kWaves = 4;                          // independent tile streams per workgroup
+constexpr int kThreads = 64 * kWaves;
+constexpr int kOPitch = kDim + 4;                  // floats per row of the merge buffer
+constexpr int kBtCache = 1024;                     // block-table entries of a split kept in LDS
 
-__device__ __forceinline__ int row_ofs(int r) { return (r >> 1) * kPair + (r & 1) * 512; }
+__device__ __forceinline__ int vrow(int r) { return 16 * r + 8 * (r & 16); }
 
 struct PartialParams {
     const _Float16* q;
@@ -108,6 +117,7 @@ struct PartialParams {
     int Hq;
     int window;              // > 0: sliding window, else none
     int causal;
+    int bs_shift;            // log2(block_size) if it is a power of two, else -1
 };
 
 struct CombineParams {
@@ -144,26 +154,12 @@ __device__ __forceinline__ half8_t widen_i8x8(unsigned w0, unsigned w1) {
 __device__ __forceinline__ float xor_max(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, 64)); }
 __device__ __forceinline__ float xor_sum(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
 
-// 16-byte HBM -> LDS DMAs: LDS[m0 + 16 * lane] = global[...]. Issued through asm so the
-// compiler does not add its conservative vmcnt(0) before every LDS read; completion is awaited
-// explicitly with wait_vm. dma16_s: scalar base + per-lane 32-bit offset; dma16_v: per-lane address.
-__device__ __forceinline__ void dma16_s(const int8_t* sbase, unsigned voff, unsigned m0) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ void dma16_v(const int8_t* vaddr, unsigned m0) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(vaddr), "s"(m0) : "memory", "m0");
-}
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 // Block-table access of one workgroup: the slice of pages its split can touch is staged in
 // LDS when it fits (kBtCache entries), so the tile loop issues no loads of its own besides the
-// K/V DMAs; otherwise entries are read with scalar loads through the constant address space.
+// K/V rows; otherwise entries are read with scalar loads through the constant address space.
 struct PageTable {
-    const lds_int* lds;  // slice [pfirst, pfirst + kBtCache)
+    const lds_int* lds;      // slice [pfirst, pfirst + kBtCache)
+    const lds_ull2* rows16;  // fast layout: per tile, the first-row offsets of its two 16-key blocks
     const_int_ptr glob;  // this sequence's block-table row
     int pfirst;
     int in_lds;
@@ -184,87 +180,103 @@ struct PageTable {
     }
 };
 
-// The 17 DMAs of one tile into the LDS image at lds_tile. voff_pair = h * k_ss + 16 * (lane & 31).
-// kFastBT (block_size 16, or even and >= 32): a tile's keys span at most two pages and both rows
-// of a pair share a page, so every instruction takes a scalar base. Rows whose key is not
-// visible are pointed at a visible page (their slot's row is read and masked later), so a freed
-// page is never addressed. Otherwise each lane addresses its own row (keys clamped into the
-// visible range) and the pair addresses are exchanged with readlane.
-template <bool kFastBT, bool kLds, int NRB>
-__device__ __forceinline__ void issue_tile(const PartialParams& a, const PageTable& pt, int tile, int lo, int hi,
-                                           int g, int lane, unsigned lds_tile, unsigned voff_pair, int part) {
-    // The NRB waves of a tile group share the 17 DMAs: wave `part` issues i = part, part + NRB, ...
+// Registers holding one tile for this lane while it is in flight and in use.
+//   k[u][c]: row 16 u + li of the tile, bytes [64 c + 16 lg, +16): the K operand of S^T = K Q^T
+//   v[u][c]: the same rows, bytes [256 + 64 c + 16 lg, +16): k_scale and V, bound for LDS
+//   t:       row 16 ((lane >> 4) & 1) + li, bytes [504, 520): the end of V and v_scale
+struct TileRegs {
+    uint4_t k[2][4];
+    uint4_t v[2][4];
+    uint4_t t;
+};
+
+// Where a tile's rows live for this lane: row 16 u + li of the tile at base[u] + row_off.
+// kFast (block_size a multiple of 16): a 16-key row block sits in one page, base[u] is the
+// block's first row (uniform) and row_off = li * k_ss. Otherwise base[u] is this lane's own row
+// and row_off = 0. Keys outside [lo, hi) are replaced by visible ones of the same tile (their
+// scores are masked), so a freed page is never addressed.
+struct TileSrc {
+    const int8_t* base[2];
+};
+
+template <bool kFast, bool kLds>
+__device__ __forceinline__ TileSrc tile_src(const PartialParams& a, const PageTable& pt, const int8_t* gbase,
+                                            int tile, int tb, int lo, int hi, int li) {
+    if constexpr (kFast && kLds) {
+        // precomputed when the split started: one LDS read, no address arithmetic. The halves
+        // are zero-extended (readfirstlane returns a signed int).
+        const ull2_t r2 = pt.rows16[tile - tb];
+        const uint64_t o0 = ((uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((unsigned)(r2.x >> 32)) << 32) |
+                            (uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((unsigned)r2.x);
+        const uint64_t o1 = ((uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((unsigned)(r2.y >> 32)) << 32) |
+                            (uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((unsigned)r2.y);
+        TileSrc src;
+        src.base[0] = gbase + (int64_t)o0;
+        src.base[1] = gbase + (int64_t)o1;
+        return src;
+    }
     const int kb = tile * kTile;
     const int kfirst = max(kb, lo), klast = min(kb + kTile - 1, hi - 1);
     const int bs = a.block_size;
-    const int rho = lane & 31, h = lane >> 5;
-    const int8_t* gbase = a.kc + (int64_t)g * a.k_sh;
-    if constexpr (kFastBT) {
-        const int lbA = kfirst / bs, lbB = klast / bs;  // lbB <= lbA + 1
-        const int8_t* pA = gbase + pt.get_uniform<kLds>(lbA) * a.k_sb;
-        const int8_t* pB = gbase + pt.get_uniform<kLds>(lbB) * a.k_sb;
-        const int lb0 = kb / bs, s0 = kb - lb0 * bs;  // page / slot of the tile's first key
-        // rows before the tile's first page boundary live at bf + key * k_ss, the rest at
-        // bw + key * k_ss (key = 0..31 inside the tile; at most one boundary since bs >= 16)
-        const int8_t* bf = (lb0 > lbA ? pB : pA) + (int64_t)s0 * a.k_ss;
-        const int8_t* bw = (lb0 + 1 > lbA ? pB : pA) - (int64_t)(bs - s0) * a.k_ss;
-        const int64_t k2 = 2 * a.k_ss;
-        for (int i = part; i < 16; i += NRB)
-            dma16_s((s0 + 2 * i < bs ? bf : bw) + (int64_t)i * k2, voff_pair, lds_tile + i * kPair);
-        if (part == 16 % NRB) {
-            int slot = s0 + rho, lb = lb0;
-            if (slot >= bs) {
-                slot -= bs;
-                lb += 1;
-            }
-            dma16_v((lb > lbA ? pB : pA) + (int64_t)slot * a.k_ss + 504, lds_tile + kTailOfs);
+    TileSrc src;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        if constexpr (kFast) {
+            const int key0 = min(max(kb + 16 * u, kfirst), klast) & ~15;
+            const int lb = a.bs_shift >= 0 ? key0 >> a.bs_shift : key0 / bs;
+            src.base[u] = gbase + pt.get_uniform<kLds>(lb) * a.k_sb + (int64_t)(key0 - lb * bs) * a.k_ss;
+        } else {
+            const int key = min(max(kb + 16 * u + li, kfirst), klast);
+            const int lb = a.bs_shift >= 0 ? key >> a.bs_shift : key / bs;
+            src.base[u] = gbase + pt.get<kLds>(lb) * a.k_sb + (int64_t)(key - lb * bs) * a.k_ss;
         }
-    } else {
-        const int t = min(max(kb + rho, kfirst), klast);
-        const int lb = t / bs;
-        const int8_t* rowp = gbase + pt.get<kLds>(lb) * a.k_sb + (int64_t)(t - lb * bs) * a.k_ss;
-        const uint64_t ra = (uint64_t)(uintptr_t)rowp;
-        const unsigned lo32 = (unsigned)ra, hi32 = (unsigned)(ra >> 32);
-        for (int i = part; i < 16; i += NRB) {
-            const unsigned l0 = __builtin_amdgcn_readlane(lo32, 2 * i);
-            const unsigned h0 = __builtin_amdgcn_readlane(hi32, 2 * i);
-            const unsigned l1 = __builtin_amdgcn_readlane(lo32, 2 * i + 1);
-            const unsigned h1 = __builtin_amdgcn_readlane(hi32, 2 * i + 1);
-            const uint64_t rr = h ? (((uint64_t)h1 << 32) | l1) : (((uint64_t)h0 << 32) | l0);
-            dma16_v((const int8_t*)(uintptr_t)(rr + 16u * (unsigned)rho), lds_tile + i * kPair);
-        }
-        if (part == 16 % NRB) dma16_v(rowp + 504, lds_tile + kTailOfs);
     }
+    return src;
 }
 
-// Workgroup shape for NRB row blocks: TG tile groups; the NRB waves of a tile group share
-// every tile (one LDS image, DMAs split between them) and each owns one row block, so a wave
-// holds only its own 16 rows of Q and O and two waves run on every SIMD.
-template <int NRB>
-struct Shape {
-    static constexpr int TG = NRB <= 2 ? 4 : 2;
-    static constexpr int kWavesWG = TG * NRB;
-    static constexpr int kThreadsWG = 64 * kWavesWG;
-    static constexpr int kLdsTiles = TG * 2 * kTileBytes;                    // double buffer per group
-    static constexpr int kLdsMerge = NRB * TG * 16 * kOPitch * 4;           // aliases the tiles
-    static constexpr int kLdsUnion = kLdsTiles > kLdsMerge ? kLdsTiles : kLdsMerge;
-    static constexpr int kLdsStats = kLdsUnion;                             // wm / wl [NRB][TG][16]
-    static constexpr int kLdsBt = kLdsStats + 2 * NRB * TG * 16 * 4;
-    static constexpr int kLdsBytes = kLdsBt + kBtCache * 4;
-    static_assert(kLdsBytes <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
-};
+__device__ __forceinline__ uint4_t ld16(const int8_t* p) { return *reinterpret_cast<const uint4_t*>(p); }
 
-template <int NRB, bool kFastBT>
-__global__ void __launch_bounds__(Shape<NRB>::kThreadsWG, 1)
-pd_partial_kernel(const PartialParams a) {
-    using S = Shape<NRB>;
-    constexpr int TG = S::TG;
-    __shared__ __attribute__((aligned(16))) unsigned char lds[S::kLdsBytes];
+// V half (and tail) of a tile: 9 loads of 16 bytes per lane.
+__device__ __forceinline__ void load_v(const TileSrc& src, unsigned lane_off, unsigned tail_off, int lane,
+                                       TileRegs& r) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) r.v[u][c] = ld16(src.base[u] + lane_off + 256 + 64 * c);
+    // row 16 u + li with u = bit 4 of the lane: select the base arithmetically (an indexed
+    // select of src.base would go through scratch)
+    const int64_t delta = src.base[1] - src.base[0];
+    const int64_t pick = -(int64_t)((lane >> 4) & 1);
+    r.t = ld16(src.base[0] + (delta & pick) + tail_off);
+}
+
+// K half of a tile: 8 loads of 16 bytes per lane, straight into the MFMA operand layout.
+__device__ __forceinline__ void load_k(const TileSrc& src, unsigned lane_off, TileRegs& r) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) r.k[u][c] = ld16(src.base[u] + lane_off + 64 * c);
+}
+
+// One workgroup = kWaves independent waves. Wave w of split s streams tiles tb + w, tb + w + 4,
+// ... of the split and computes all R query rows of the kv head for each (NRB row blocks of
+// 16), so every K/V byte is loaded and widened once. Loads run one tile ahead in registers:
+// tile n + 1 is issued as soon as tile n's registers are free (its V half once written to LDS,
+// its K half once S is computed), so every wave keeps a tile in flight while it computes.
+template <int NRB, bool kFast>
+__global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialParams a) {
+    constexpr int kLdsWaves = kWaves * kWaveLds;
+    constexpr int kLdsMerge = kWaves * 16 * kOPitch * 4;  // one row block of every wave, aliases the images
+    constexpr int kLdsMain = kLdsWaves > kLdsMerge ? kLdsWaves : kLdsMerge;
+    constexpr int kLdsStats = kLdsMain;                   // m, l: [wave][NRB][16]
+    constexpr int kLdsBt = kLdsStats + 2 * kWaves * NRB * 16 * 4;
+    constexpr int kLdsBytes = kLdsBt + kBtCache * 8;
+    static_assert(kLdsBytes <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
 
     const int s = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, l = tid & 63, lg = l >> 4, li = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, uniform by construction
-    const int rb = w % NRB, tg = w / NRB;                     // this wave's row block and tile group
 
     const int q0 = a.qsl[b];
     const int q_len = a.qsl[b + 1] - q0;
@@ -288,56 +300,66 @@ pd_partial_kernel(const PartialParams a) {
     };
 
     if (tb >= te) {  // no tiles: mark the split empty for the combine
-        for (int r = tid; r < R; r += S::kThreadsWG) {
+        for (int r = tid; r < R; r += kThreads) {
             a.part_m[prow(r)] = kNegInf;
             a.part_l[prow(r)] = 0.f;
         }
         return;
     }
 
-    // ---- this wave's 16 query rows and their Q^T operand (B of S^T = K Q^T) ----
-    const int r = 16 * rb + li;
-    const bool rvalid = r < R;
-    const int qi = r / G, qh = r - (r / G) * G;
-    const int rpos = ctx0 + qi;
-    half8_t qop[8];
-    float qs = 0.f;  // sum of the row's 256 fp16 query values (64 per lane group)
-    {
-        const _Float16* qrow = a.q + (int64_t)(q0 + (rvalid ? qi : 0)) * a.q_st + (int64_t)(g * G + qh) * kDim;
+    // ---- Q^T operand (B of S^T = K Q^T) of every row block; lane (lg, li) holds row 16 rb + li,
+    //      dims 64 (st / 2) + 16 lg + 8 (st % 2) + [0, 8) in qop[rb][st] ----
+    half8_t qop[NRB][8];
+    float qcorr[NRB];
+    bool rvalid[NRB];
+    int rpos[NRB];
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) {
+        const int r = 16 * rb + li;
+        rvalid[rb] = r < R;
+        const int qi = r / G, qh = r - (r / G) * G;
+        rpos[rb] = ctx0 + qi;
+        float qs = 0.f;
+        const _Float16* qrow =
+            a.q + (int64_t)(q0 + (rvalid[rb] ? qi : 0)) * a.q_st + (int64_t)(g * G + (rvalid[rb] ? qh : 0)) * kDim;
 #pragma unroll
         for (int st = 0; st < 8; ++st) {
             half8_t v;
             const int dim = 64 * (st >> 1) + 16 * lg + 8 * (st & 1);
             __builtin_memcpy(&v, __builtin_assume_aligned(qrow + dim, 4), 16);
-            qop[st] = rvalid ? v : (half8_t)(_Float16)0.0f;
+            qop[rb][st] = rvalid[rb] ? v : (half8_t)(_Float16)0.0f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) qs += (float)qop[st][e];
+            for (int e = 0; e < 8; ++e) qs += (float)qop[rb][st][e];
         }
+        qcorr[rb] = kWidenBias * xor_sum(xor_sum(qs, 16), 32);  // widening bias of K, per row
     }
-    const float qcorr = kWidenBias * xor_sum(xor_sum(qs, 16), 32);
 
-    // Running state of the wave's rows: max (log2 units), this lane's partial sums of p and of
-    // the fp16 P' values (the latter removes the widening bias from O), and O^T.
-    float m_run = kNegInf, l_run = 0.f, cp_run = 0.f;
-    float4_t oacc[17];
+    // Running state per row block: max (log2 units), this lane's partial sum of p, and O^T in
+    // 17 blocks of 16 "dims" (block m < 16: dims 16 m - 4 .. 16 m + 11; block 16: dims 244..255,
+    // then 1152 * sum P' in lane group 3, the widening bias of V to remove at the end).
+    float m_run[NRB], l_run[NRB];
+    float4_t oacc[NRB][17];
 #pragma unroll
-    for (int m = 0; m < 17; ++m) oacc[m] = (float4_t)0.f;
+    for (int rb = 0; rb < NRB; ++rb) {
+        m_run[rb] = kNegInf;
+        l_run[rb] = 0.f;
+#pragma unroll
+        for (int m = 0; m < 17; ++m) oacc[rb][m] = (float4_t)0.f;
+    }
 
     lds_u8* L = (lds_u8*)lds;
-    const unsigned lds_base = (unsigned)(uintptr_t)L;
-    const unsigned gofs = (unsigned)(tg * 2 * kTileBytes);  // this tile group's double buffer
-    // LDS offsets (inside a tile image) this lane reads, all fixed for the kernel:
-    //   K operand: key rows li and li + 16, bytes [16 lg, ...) of each 64-byte column group
-    const int k_ofs0 = row_ofs(li) + 16 * lg, k_ofs1 = row_ofs(li + 16) + 16 * lg;
-    //   transposed V reads: lane pair (2r, 2r+1) of a 16-lane group names key slot r
-    const int slot = li >> 1;
-    const int tkey = slot < 4 ? 4 * lg + slot : 16 + 4 * lg + (slot - 4);
-    const int v_ofs = row_ofs(tkey) + 256 + 8 * (li & 1);
-    const int vt_ofs = kTailOfs + 16 * tkey + 8 * (li & 1);
-    //   scales of this lane's S^T keys 16u + 4lg + j: k_scale at row byte 256, v_scale in the tail
-    const int ks_ofs = row_ofs(4 * lg) + 256;
-    const int vs_ofs = kTailOfs + 16 * (4 * lg) + 12;
-    const unsigned voff_pair = (unsigned)((l >> 5) * a.k_ss) + 16u * (unsigned)(l & 31);
+    lds_u8* V = L + w * kWaveLds;  // this wave's V image
+    lds_float* KS = (lds_float*)(V + kScalesOfs);
+    lds_float* VS = KS + kTile;
+    // transposed V reads: lane pair (2 i, 2 i + 1) of a 16-lane group names tile row tkey
+    const int tslot = li >> 1;
+    const int tkey = tslot < 4 ? 4 * lg + tslot : 16 + 4 * lg + (tslot - 4);
+    const int vt_ofs = vrow(tkey) + 8 * (li & 1);
+
+    const int8_t* gbase = a.kc + (int64_t)g * a.k_sh;
+    const unsigned row_off = kFast ? (unsigned)(li * a.k_ss) : 0u;
+    const unsigned lane_off = row_off + 16u * (unsigned)lg;
+    const unsigned tail_off = row_off + 504u;
 
     // The block table is read-only for the kernel's lifetime: read it through the constant
     // address space so uniform lookups become scalar loads.
@@ -347,155 +369,215 @@ pd_partial_kernel(const PartialParams a) {
     {
         const int pk_first = max(tb * kTile, lo), pk_last = min(te * kTile, hi) - 1;
         pt.pfirst = pk_first / a.block_size;
-        const int npages = pk_last / a.block_size - pt.pfirst + 1;
-        pt.in_lds = npages <= kBtCache;
-        pt.lds = (const lds_int*)(L + S::kLdsBt);
-        if (pt.in_lds) {
-            lds_int* dst = (lds_int*)(L + S::kLdsBt);
-            for (int i = tid; i < npages; i += S::kThreadsWG)
-                dst[i] = a.block_table[(int64_t)b * a.bt_stride + pt.pfirst + i];
+        pt.lds = (const lds_int*)(L + kLdsBt);
+        pt.rows16 = (const lds_ull2*)(L + kLdsBt);
+        const int* bt_glob = a.block_table + (int64_t)b * a.bt_stride;
+        if constexpr (kFast) {
+            // byte offset (from this kv head's base) of the first row of every 16-key block of
+            // the split, two per tile; blocks outside [lo, hi) point at a visible block of the tile
+            const int nblk = 2 * (te - tb);
+            pt.in_lds = nblk <= kBtCache;
+            if (pt.in_lds) {
+                lds_u64* dst = (lds_u64*)(L + kLdsBt);
+                for (int i = tid; i < nblk; i += kThreads) {
+                    const int kb = (tb + (i >> 1)) * kTile;
+                    const int kfirst = max(kb, lo), klast = min(kb + kTile - 1, hi - 1);
+                    const int key0 = min(max(kb + 16 * (i & 1), kfirst), klast) & ~15;
+                    const int lb = key0 / a.block_size;
+                    dst[i] = (uint64_t)((int64_t)bt_glob[lb] * a.k_sb + (int64_t)(key0 - lb * a.block_size) * a.k_ss);
+                }
+            }
+        } else {
+            const int npages = pk_last / a.block_size - pt.pfirst + 1;
+            pt.in_lds = npages <= kBtCache;
+            if (pt.in_lds) {
+                lds_int* dst = (lds_int*)(L + kLdsBt);
+                for (int i = tid; i < npages; i += kThreads) dst[i] = bt_glob[pt.pfirst + i];
+            }
         }
         __syncthreads();
     }
 
-    // tiles of this tile group: tb + tg + n * TG, n < nt_max (all waves run nt_max iterations
-    // so that they meet at the same barriers)
-    const int nt_max = (te - tb + TG - 1) / TG;
-    auto tile_of = [&](int n) { return tb + tg + n * TG; };
+    const int nt = max(0, (te - tb - w + kWaves - 1) / kWaves);  // tiles of this wave
+    auto tile_of = [&](int n) { return tb + w + kWaves * n; };
 
-    // ---- scores of one tile: S^T = K Q^T (two interleaved MFMA chains), times k_scale, minus
-    //      the widening bias; sv = -inf where masked; returns this lane's max ----
-    auto tile_scores = [&](int tile, const lds_u8* T, float (&sv)[8], bool& interior) __attribute__((always_inline)) {
-        uint4_t kraw[2][4];
+    // ---- tile n's V half and scales into the LDS image ----
+    auto store_v = [&](const TileRegs& r) __attribute__((always_inline)) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            kraw[0][c] = *(const lds_uint4*)(T + k_ofs0 + 64 * c);
-            kraw[1][c] = *(const lds_uint4*)(T + k_ofs1 + 64 * c);
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                *(lds_uint4*)(V + (4 * c + lg) * kVPitch + vrow(16 * u + li)) = r.v[u][c];
+        // (vector elements are copied to scalars before __builtin_bit_cast: clang lowers a bit
+        // cast of a vector-element lvalue to a load from the vector's first element)
+        if (lg == 0) {
+            const unsigned k0 = r.v[0][0].x, k1 = r.v[1][0].x;
+            KS[li] = __builtin_bit_cast(float, k0);
+            KS[16 + li] = __builtin_bit_cast(float, k1);
         }
-        float4_t sacc[2];
+        if (l < 32) {
+            const int tr = 16 * (l >> 4) + li;
+            const unsigned vw = r.t.w;
+            VS[tr] = __builtin_bit_cast(float, vw);
+            uint4_t t = r.t;
+            t.w = 0u;  // cleared v_scale bytes: that MFMA output row becomes 1152 * sum P'
+            *(lds_uint4*)(V + 16 * kVPitch + vrow(tr)) = t;
+        }
+    };
+
+    // ---- S^T = K Q^T for every row block, times k_scale, minus the widening bias; masked
+    //      scores are -inf. Returns whether some row's tile max exceeds its running max + kLazy ----
+    auto tile_scores = [&](int tile, const TileRegs& r, float (&sv)[NRB][8], bool& interior)
+        __attribute__((always_inline)) {
+        float4_t sacc[NRB][2];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
-                    const half8_t kf = hh == 0 ? widen_i8x8(kraw[u][c].x, kraw[u][c].y)
-                                               : widen_i8x8(kraw[u][c].z, kraw[u][c].w);
-                    sacc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qop[2 * c + hh],
-                                                                     (c | hh) ? sacc[u] : (float4_t)0.f, 0, 0, 0);
+                    const uint4_t kr = r.k[u][c];
+                    const half8_t kf = hh == 0 ? widen_i8x8(kr.x, kr.y) : widen_i8x8(kr.z, kr.w);
+#pragma unroll
+                    for (int rb = 0; rb < NRB; ++rb)
+                        sacc[rb][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            kf, qop[rb][2 * c + hh], (c | hh) ? sacc[rb][u] : (float4_t)0.f, 0, 0, 0);
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);  // bounds the operands widened ahead of their MFMAs
         }
         float ks[8];
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                ks[4 * u + j] = *(const lds_float*)(T + ks_ofs + row_ofs(16 * u + j)) * a.scale_log2;
+            for (int j = 0; j < 4; ++j) ks[4 * u + j] = KS[16 * u + 4 * lg + j] * a.scale_log2;
         const int kb = tile * kTile;
         // Interior tile: every key is visible to every row (padding rows have Q = 0 and are
         // never written out), so no per-element mask is needed.
         interior = kb >= lo && kb + kTile <= hi;
         if (a.causal) interior = interior && kb + kTile - 1 <= ctx0;
         if (a.window > 0) interior = interior && (ctx0 + ql - 1) - kb < a.window;
-        float mx = kNegInf;
-        if (interior) {
+        bool need = false;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                sv[e] = (sacc[e >> 2][e & 3] - qcorr) * ks[e];
-                mx = fmaxf(mx, sv[e]);
-            }
-        } else {
+        for (int rb = 0; rb < NRB; ++rb) {
+            float mx = kNegInf;
+            if (interior) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int t = kb + 16 * (e >> 2) + 4 * lg + (e & 3);
-                const bool vis = rvalid & (t >= lo) & (t < hi) & (!a.causal | (t <= rpos)) &
-                                 ((a.window <= 0) | ((rpos - t) < a.window));
-                sv[e] = vis ? (sacc[e >> 2][e & 3] - qcorr) * ks[e] : kNegInf;
-                mx = fmaxf(mx, sv[e]);
+                for (int e = 0; e < 8; ++e) {
+                    sv[rb][e] = (sacc[rb][e >> 2][e & 3] - qcorr[rb]) * ks[e];
+                    mx = fmaxf(mx, sv[rb][e]);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int t = kb + 16 * (e >> 2) + 4 * lg + (e & 3);
+                    const int rp = rpos[rb];
+                    const bool vis = rvalid[rb] & (t >= lo) & (t < hi) & (!a.causal | (t <= rp)) &
+                                     ((a.window <= 0) | ((rp - t) < a.window));
+                    sv[rb][e] = vis ? (sacc[rb][e >> 2][e & 3] - qcorr[rb]) * ks[e] : kNegInf;
+                    mx = fmaxf(mx, sv[rb][e]);
+                }
             }
+            need |= mx > m_run[rb] + kLazy;
         }
-        return mx;
+        return need;
     };
 
-    // ---- P' = 2^(s - m) * v_scale * 16 (fp16), then O^T += V^T P'^T ----
-    auto tile_values = [&](const lds_u8* T, const float (&sv)[8], bool interior) __attribute__((always_inline)) {
-        float psum = 0.f, csum = 0.f;
-        _Float16 pv[8];
+    // rare path: raise the running max of the rows that need it and rescale their state
+    auto raise_max = [&](const float (&sv)[NRB][8]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int rb = 0; rb < NRB; ++rb) {
+            float mloc = kNegInf;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int e = 4 * u + j;
-                const float vsc = *(const lds_float*)(T + vs_ofs + 16 * (16 * u + j)) * kPScale;
-                // masked scores are -inf; the select also keeps a NaN scale of a masked row out
-                const bool vis = interior || sv[e] > kNegInf;
-                const float p = vis ? __builtin_amdgcn_exp2f(sv[e] - m_run) : 0.f;
-                psum += p;
-                pv[e] = (_Float16)(vis ? p * vsc : 0.f);
-                csum += (float)pv[e];
-            }
+            for (int e = 0; e < 8; ++e) mloc = fmaxf(mloc, sv[rb][e]);
+            const float mrow = xor_max(xor_max(mloc, 16), 32);
+            const float m_new = mrow > m_run[rb] + kLazy ? mrow : m_run[rb];
+            const float alpha = m_run[rb] == kNegInf ? 0.f : __builtin_amdgcn_exp2f(m_run[rb] - m_new);
+            m_run[rb] = m_new;
+            l_run[rb] *= alpha;
+#pragma unroll
+            for (int m = 0; m < 17; ++m) oacc[rb][m] *= alpha;
         }
-        l_run += psum;
-        cp_run += csum;
-        const half8_t pop = half8_t{pv[0], pv[1], pv[2], pv[3], pv[4], pv[5], pv[6], pv[7]};
+    };
+
+    // ---- P' = 2^(s - m) * v_scale * 16 as two fp16 parts (hi + lo, ~22 significant bits: a
+    //      single fp16 would put 2^-12 relative error on every term, too much next to outlier V
+    //      rows), then O^T += V^T hi^T + V^T lo^T for every row block ----
+    auto tile_values = [&](const float (&sv)[NRB][8], bool interior) __attribute__((always_inline)) {
+        float vsc[8];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) vsc[4 * u + j] = VS[16 * u + 4 * lg + j] * kPScale;
+        half8_t phi[NRB], plo[NRB];
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) {
+            float psum = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                // masked scores are -inf; the select also keeps a NaN scale of a masked row out
+                const bool vis = interior || sv[rb][e] > kNegInf;
+                const float p = vis ? __builtin_amdgcn_exp2f(sv[rb][e] - m_run[rb]) : 0.f;
+                psum += p;
+                const float pv = vis ? p * vsc[e] : 0.f;
+                const _Float16 h = (_Float16)pv;
+                phi[rb][e] = h;
+                plo[rb][e] = (_Float16)(pv - (float)h);
+            }
+            l_run[rb] += psum;
+        }
 #pragma unroll
         for (int m = 0; m < 17; ++m) {
-            const int ofs = m < 16 ? v_ofs + 16 * m : vt_ofs;
-            const int2_t raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_int2*)(T + ofs));
-            oacc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(widen_i8x8((unsigned)raw.x, (unsigned)raw.y), pop,
-                                                             oacc[m], 0, 0, 0);
+            const int2_t raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_int2*)(V + m * kVPitch + vt_ofs));
+            const half8_t vf = widen_i8x8((unsigned)raw.x, (unsigned)raw.y);
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb)
+                oacc[rb][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, phi[rb], oacc[rb][m], 0, 0, 0);
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb)
+                oacc[rb][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, plo[rb], oacc[rb][m], 0, 0, 0);
+            if ((m & 3) == 3) __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    // Tile loop. Per iteration: wait for this wave's DMAs of the current tile, meet the other
-    // waves (the whole tile has landed, and every wave is done with the other buffer), issue this
-    // wave's share of the next tile's DMAs into that buffer, compute. The fast inner loop has no
-    // rescale: a row's running max is raised only when a tile's score exceeds it by more than
-    // kLazy (one ballot decides), and then the loop is left, the rows are rescaled with the
-    // cross-lane row max, the tile is finished and the loop resumes. This keeps the O
-    // accumulators in AGPRs, untouched by the vector ALU, on the common path.
+    // ---- the tile stream of this wave ----
     auto tile_loop = [&](auto lds_flag) __attribute__((always_inline)) {
         constexpr bool kLds = decltype(lds_flag)::value;
-        if (tile_of(0) < te)
-            issue_tile<kFastBT, kLds, NRB>(a, pt, tile_of(0), lo, hi, g, l, lds_base + gofs, voff_pair, rb);
-        int n = 0;
-        float sv[8];
+        auto src_of = [&](int n) __attribute__((always_inline)) {
+            return tile_src<kFast, kLds>(a, pt, gbase, tile_of(n), tb, lo, hi, li);
+        };
+        TileRegs r;
+        if (nt > 0) {
+            const TileSrc first = src_of(0);
+            load_v(first, lane_off, tail_off, l, r);
+            load_k(first, lane_off, r);
+        }
+        // The fast inner loop never rescales: O stays in the MFMA accumulators, untouched by
+        // the vector ALU. When some row's max must be raised the loop is left, the rows are
+        // rescaled, the tile is finished and the loop resumes with the next tile, whose loads
+        // are already in flight.
+        float sv[NRB][8];
         bool interior = true;
-        const lds_u8* T = L;
-        while (n < nt_max) {
+        int n = 0;
+        while (n < nt) {
             bool rare = false;
-            for (; n < nt_max; ++n) {
-                wait_vm<0>();
-                __syncthreads();
-                if (tile_of(n + 1) < te) {
-                    const unsigned nxt = gofs + (unsigned)(((n + 1) & 1) * kTileBytes);
-                    issue_tile<kFastBT, kLds, NRB>(a, pt, tile_of(n + 1), lo, hi, g, l, lds_base + nxt, voff_pair,
-                                                   rb);
-                }
-                if (tile_of(n) >= te) continue;
-                T = L + gofs + (n & 1) * kTileBytes;
-                const float mloc = tile_scores(tile_of(n), T, sv, interior);
-                if (__builtin_amdgcn_ballot_w64(mloc > m_run + kLazy) != 0) {
+            for (; n < nt; ++n) {
+                const bool more = n + 1 < nt;
+                TileSrc nxt;
+                if (more) nxt = src_of(n + 1);
+                store_v(r);
+                if (more) load_v(nxt, lane_off, tail_off, l, r);  // V of tile n + 1 into the freed registers
+                const bool need = tile_scores(tile_of(n), r, sv, interior);
+                if (more) load_k(nxt, lane_off, r);  // K of tile n + 1, once S of tile n is computed
+                if (__builtin_amdgcn_ballot_w64(need) != 0) {
                     rare = true;
                     break;
                 }
-                tile_values(T, sv, interior);
+                tile_values(sv, interior);
             }
             if (!rare) break;
-            // rare path: raise the running max of the rows that need it, rescale, finish the tile
-            float mloc = kNegInf;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) mloc = fmaxf(mloc, sv[e]);
-            const float mrow = xor_max(xor_max(mloc, 16), 32);
-            const float m_new = mrow > m_run + kLazy ? mrow : m_run;
-            const float alpha = m_run == kNegInf ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-            m_run = m_new;
-            l_run *= alpha;
-            cp_run *= alpha;
-#pragma unroll
-            for (int m = 0; m < 17; ++m) oacc[m] *= alpha;
-            tile_values(T, sv, interior);
+            raise_max(sv);
+            tile_values(sv, interior);
             ++n;
         }
     };
@@ -503,64 +585,62 @@ pd_partial_kernel(const PartialParams a) {
         tile_loop(std::true_type{});
     else
         tile_loop(std::false_type{});
-    wait_vm<0>();
 
-    // ---- merge the TG waves of each row block through LDS and write the partials ----
-    const float l_row = xor_sum(xor_sum(l_run, 16), 32);
-    const float corr = kWidenBias * xor_sum(xor_sum(cp_run, 16), 32);  // sum of the row's P'
-    float* wm = reinterpret_cast<float*>(lds + S::kLdsStats);           // [NRB][TG][16]
-    float* wl = wm + NRB * TG * 16;
-    __syncthreads();  // every wave is done with the tile buffers (the merge buffer aliases them)
-    if (lg == 0) {
-        wm[(rb * TG + tg) * 16 + li] = m_run;
-        wl[(rb * TG + tg) * 16 + li] = l_row;
-    }
-    __syncthreads();
-    {
-        float M = kNegInf;
+    // ---- merge the waves through LDS and write one partial per row ----
+    float* wm = reinterpret_cast<float*>(lds + kLdsStats);  // [wave][NRB][16]
+    float* wl = wm + kWaves * NRB * 16;
+    float corr[NRB];
 #pragma unroll
-        for (int t = 0; t < TG; ++t) M = fmaxf(M, wm[(rb * TG + t) * 16 + li]);
-        const float f = m_run == kNegInf ? 0.f : exp2f(m_run - M) * (1.0f / kPScale);
-        float* ob = reinterpret_cast<float*>(lds) + ((rb * TG + tg) * 16 + li) * kOPitch;
-#pragma unroll
-        for (int m = 0; m < 17; ++m) {
-            // block m < 16 covers dims 16m-4 .. 16m+11, block 16 dims 244..255 (only lg == 2 is new)
-            const int d0 = m < 16 ? 16 * m - 4 + 4 * lg : (lg == 2 ? 252 : -1);
-            if (d0 >= 0 && d0 < kDim) *reinterpret_cast<float4_t*>(ob + d0) = (oacc[m] - corr) * f;
+    for (int rb = 0; rb < NRB; ++rb) {
+        const float l_row = xor_sum(xor_sum(l_run[rb], 16), 32);
+        corr[rb] = __shfl(oacc[rb][16].x, 48 + li, 64);  // 1152 * sum of the row's P'
+        if (lg == 0) {
+            wm[(w * NRB + rb) * 16 + li] = m_run[rb];
+            wl[(w * NRB + rb) * 16 + li] = l_row;
         }
     }
-    __syncthreads();
-    {
-        // thread -> (row block, row, chunk of CH dims); sum the TG tile groups
-        constexpr int CH = 4096 / (S::kThreadsWG / NRB);
-        const int orb = tid / (S::kThreadsWG / NRB), idx = tid % (S::kThreadsWG / NRB);
-        const int orow = idx / (kDim / CH), dq = (idx % (kDim / CH)) * CH;
-        const int rr = 16 * orb + orow;
-        if (rr < R) {
-            float Mr = kNegInf;
+    __syncthreads();  // stats visible; every wave is done with its V image (the slab aliases them)
+    float* slab = reinterpret_cast<float*>(lds);  // [wave][16 rows][kOPitch]
+    const int orow = tid >> 4, dq = (tid & 15) * 16;  // merge thread: row, 16 dims
 #pragma unroll
-            for (int t = 0; t < TG; ++t) Mr = fmaxf(Mr, wm[(orb * TG + t) * 16 + orow]);
+    for (int rb = 0; rb < NRB; ++rb) {
+        float M = kNegInf;
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) M = fmaxf(M, wm[(v * NRB + rb) * 16 + li]);
+        const float f = m_run[rb] == kNegInf ? 0.f : exp2f(m_run[rb] - M) * (1.0f / kPScale);
+        float* ob = slab + (w * 16 + li) * kOPitch;
+#pragma unroll
+        for (int m = 0; m < 17; ++m) {
+            const int d0 = m < 16 ? 16 * m - 4 + 4 * lg : (lg == 2 ? 252 : -1);
+            if (d0 >= 0 && d0 < kDim) *reinterpret_cast<float4_t*>(ob + d0) = (oacc[rb][m] - corr[rb]) * f;
+        }
+        __syncthreads();
+        const int rr = 16 * rb + orow;
+        if (rr < R) {
             float* dst = a.part_o + prow(rr) * kDim + dq;
 #pragma unroll
-            for (int q4 = 0; q4 < CH / 4; ++q4) {
+            for (int q4 = 0; q4 < 4; ++q4) {
                 float4_t acc = (float4_t)0.f;
 #pragma unroll
-                for (int t = 0; t < TG; ++t)
-                    acc += *reinterpret_cast<const float4_t*>(reinterpret_cast<const float*>(lds) +
-                                                              ((orb * TG + t) * 16 + orow) * kOPitch + dq + 4 * q4);
+                for (int v = 0; v < kWaves; ++v)
+                    acc += *reinterpret_cast<const float4_t*>(slab + (v * 16 + orow) * kOPitch + dq + 4 * q4);
                 *reinterpret_cast<float4_t*>(dst + 4 * q4) = acc;
             }
             if (dq == 0) {
+                float Mr = kNegInf;
+#pragma unroll
+                for (int v = 0; v < kWaves; ++v) Mr = fmaxf(Mr, wm[(v * NRB + rb) * 16 + orow]);
                 float Lr = 0.f;
 #pragma unroll
-                for (int t = 0; t < TG; ++t) {
-                    const float mw = wm[(orb * TG + t) * 16 + orow];
-                    if (mw != kNegInf) Lr += exp2f(mw - Mr) * wl[(orb * TG + t) * 16 + orow];
+                for (int v = 0; v < kWaves; ++v) {
+                    const float mw = wm[(v * NRB + rb) * 16 + orow];
+                    if (mw != kNegInf) Lr += exp2f(mw - Mr) * wl[(v * NRB + rb) * 16 + orow];
                 }
                 a.part_m[prow(rr)] = Mr;
                 a.part_l[prow(rr)] = Lr;
             }
         }
+        __syncthreads();  // the slab is rewritten for the next row block
     }
 }
 
@@ -687,7 +767,9 @@ struct LaunchArgs {
     int window, causal;
 };
 
-bool fast_block_table(int bs) { return bs == 16 || (bs >= 32 && bs % 2 == 0); }
+// Row blocks of 16 keys never straddle a page when block_size is a multiple of 16: then every
+// row block of a tile has one scalar base address.
+bool fast_block_table(int bs, int64_t k_ss) { return bs % 16 == 0 && k_ss < (int64_t(1) << 27); }
 
 hipError_t check_args(const LaunchArgs& x, bool strict_reference) {
     if (x.heads_kv < 1 || x.heads_q < 1 || x.heads_q % x.heads_kv != 0) return hipErrorInvalidValue;
@@ -705,7 +787,7 @@ hipError_t check_args(const LaunchArgs& x, bool strict_reference) {
 
 template <int NRB>
 hipError_t launch_partial_nrb(const PartialParams& p, dim3 grid, hipStream_t stream, bool fast) {
-    const dim3 block(Shape<NRB>::kThreadsWG);
+    const dim3 block(kThreads);
     if (fast)
         hipLaunchKernelGGL((pd_partial_kernel<NRB, true>), grid, block, 0, stream, p);
     else
@@ -737,9 +819,10 @@ hipError_t launch_partial(const LaunchArgs& x, hipStream_t stream) {
     p.Hq = x.heads_q;
     p.window = x.window > 0 ? x.window : 0;
     p.causal = x.causal ? 1 : 0;
+    p.bs_shift = (x.block_size & (x.block_size - 1)) == 0 ? __builtin_ctz((unsigned)x.block_size) : -1;
     const int rows = x.qmax * p.G;
     const dim3 grid(x.nsplit, x.heads_kv, x.num_seqs);
-    const bool fast = fast_block_table(x.block_size);
+    const bool fast = fast_block_table(x.block_size, x.k_ss);
     if (rows <= 16) return launch_partial_nrb<1>(p, grid, stream, fast);
     if (rows <= 32) return launch_partial_nrb<2>(p, grid, stream, fast);
     return launch_partial_nrb<3>(p, grid, stream, fast);

@@ -4,7 +4,8 @@ The expected outputs were computed once, row by row, from the definition of the 
 float64 path (kernels/pth_dec/test_dec.py:70-88) with the mask rule of
 patches/vllm/gfx906_fa_paged.patch:7-20; they are stored as float32. The oracle must reproduce
 them to float32 rounding; the HIP operator must match them to the fp16-output tolerance
-(max-abs <= 2e-3, mean-abs <= 2e-4) and write exactly the rows the oracle writes.
+(max-abs <= 2e-3, mean-abs <= 2e-4, beyond half an fp16 ulp of the expected value, which is the
+rounding of the output itself) and write exactly the rows the oracle writes.
 """
 import os
 
@@ -72,5 +73,10 @@ def test_hip_matches_golden(name, nsplit):
     w = c["written"]
     assert np.isfinite(o[w]).all()
     assert np.isnan(o[~w]).all(), "rows the operator must not write were written"
-    e = np.abs(o[w] - c["expected"][w])
-    assert e.max() <= 2e-3 and e.mean() <= 2e-4, (e.max(), e.mean())
+    exp = c["expected"][w].astype(np.float64)
+    # the output is fp16: on top of 2e-3 / 2e-4 allow half an fp16 ulp of the expected value
+    # (the outlier fixture has outputs up to ~28, where half an ulp is 7.8e-3)
+    half_ulp = np.spacing(np.abs(exp).astype(np.float16)).astype(np.float64) / 2
+    e = np.abs(o[w] - exp)
+    excess = np.maximum(e - half_ulp, 0.0)
+    assert excess.max() <= 2e-3 and excess.mean() <= 2e-4, (e.max(), excess.max(), excess.mean())
