@@ -79,22 +79,29 @@ constexpr float kNegInf = -__builtin_inff();
 constexpr float kLazy = 4.0f;
 constexpr float kPScale = 16.0f;
 
-// Per-wave LDS image of the V half of one tile. Chunk j (0..15) holds bytes
-// [256 + 16 j, 272 + 16 j) of the tile's 32 rows (chunk 0 starts with the row's k_scale), chunk
-// 16 holds bytes [504, 520) with the v_scale word cleared. Row r of a chunk sits at vrow(r)
-// (16 r, +128 for r >= 16), so the 8 rows one 16-lane group reads with ds_read_b64_tr_b8 cover
-// 32 distinct banks and a half-wave all 64.
-constexpr int kVChunks = 17;
-constexpr int kVPitch = 640;                       // bytes per chunk
-constexpr int kVImage = kVChunks * kVPitch;
-constexpr int kScalesOfs = kVImage;                // k_scale[32], then v_scale[32] (f32)
-constexpr int kWaveLds = kVImage + 2 * kTile * 4;  // LDS bytes per wave
+// LDS slot of one tile (each wave double-buffers its tiles; 17664 bytes per slot).
+//   K image, 8 DMA blocks of 1040 bytes (1024 + 16 of padding): block i holds the tile rows
+//     16 (i >> 2) + 4 (i & 3) + q, q = 0..3, bytes [0, 256); row q of the block at 256 q, its
+//     16-byte chunk c at position c ^ 4 q.
+//   V image, 8 blocks of 1040 bytes at kImgV: block i holds rows 16 (i >> 2) + (i & 3) + 4 q,
+//     bytes [256, 512) (k_scale, V[0..252)); row q at 256 q, chunk c at position c ^ 8 (q & 1).
+//   Tail, 1024 bytes at kImgT: bytes [504, 520) of row r at 16 tpos(r), tpos(r) = r for r < 16
+//     and 16 + ((r - 16) ^ 8) above (the DMA's lanes 32..63 land a copy at +512).
+// With these placements the 16 rows one 16-lane group reads for the K operand, and the 8 rows a
+// ds_read_b64_tr_b8 group reads, fall on distinct LDS banks. Each DMA block is 4 rows of 256
+// contiguous bytes of one page, so its 64 lanes share a scalar base.
+// Block sizes that are not a multiple of 16 use chunk-major images instead (chunk j of row r at
+// 512 j + 16 r), filled from per-lane row addresses.
+constexpr int kBlk = 1040;
+constexpr int kImgK = 0;
+constexpr int kImgV = 8 * kBlk;
+constexpr int kImgT = 16 * kBlk;
+constexpr int kSlot = kImgT + 1024;
+constexpr int kWaveLds = 2 * kSlot;                // LDS bytes per wave
 constexpr int kWaves = 4;                          // independent tile streams per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kOPitch = kDim + 4;                  // floats per row of the merge buffer
 constexpr int kBtCache = 1024;                     // block-table entries of a split kept in LDS
-
-__device__ __forceinline__ int vrow(int r) { return 16 * r + 8 * (r & 16); }
 
 struct PartialParams {
     const _Float16* q;
@@ -180,28 +187,17 @@ struct PageTable {
     }
 };
 
-// Registers holding one tile for this lane while it is in flight and in use.
-//   k[u][c]: row 16 u + li of the tile, bytes [64 c + 16 lg, +16): the K operand of S^T = K Q^T
-//   v[u][c]: the same rows, bytes [256 + 64 c + 16 lg, +16): k_scale and V, bound for LDS
-//   t:       row 16 ((lane >> 4) & 1) + li, bytes [504, 520): the end of V and v_scale
-struct TileRegs {
-    uint4_t k[2][4];
-    uint4_t v[2][4];
-    uint4_t t;
-};
-
-// Where a tile's rows live for this lane: row 16 u + li of the tile at base[u] + row_off.
-// kFast (block_size a multiple of 16): a 16-key row block sits in one page, base[u] is the
-// block's first row (uniform) and row_off = li * k_ss. Otherwise base[u] is this lane's own row
-// and row_off = 0. Keys outside [lo, hi) are replaced by visible ones of the same tile (their
-// scores are masked), so a freed page is never addressed.
+// Where a tile's rows live. kFast (block_size a multiple of 16, so a 16-key row block sits in
+// one page): row 16 u + x of the tile at base[u] + x * k_ss, base[u] uniform. Other block sizes:
+// base[0] is this lane's own tile row, lane & 31. Keys outside [lo, hi) are replaced by visible
+// keys of the same tile (their scores are masked), so a freed page is never addressed.
 struct TileSrc {
     const int8_t* base[2];
 };
 
 template <bool kFast, bool kLds>
 __device__ __forceinline__ TileSrc tile_src(const PartialParams& a, const PageTable& pt, const int8_t* gbase,
-                                            int tile, int tb, int lo, int hi, int li) {
+                                            int tile, int tb, int lo, int hi, int lane) {
     if constexpr (kFast && kLds) {
         // precomputed when the split started: one LDS read, no address arithmetic. The halves
         // are zero-extended (readfirstlane returns a signed int).
@@ -219,54 +215,110 @@ __device__ __forceinline__ TileSrc tile_src(const PartialParams& a, const PageTa
     const int kfirst = max(kb, lo), klast = min(kb + kTile - 1, hi - 1);
     const int bs = a.block_size;
     TileSrc src;
+    if constexpr (kFast) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        if constexpr (kFast) {
+        for (int u = 0; u < 2; ++u) {
             const int key0 = min(max(kb + 16 * u, kfirst), klast) & ~15;
             const int lb = a.bs_shift >= 0 ? key0 >> a.bs_shift : key0 / bs;
             src.base[u] = gbase + pt.get_uniform<kLds>(lb) * a.k_sb + (int64_t)(key0 - lb * bs) * a.k_ss;
-        } else {
-            const int key = min(max(kb + 16 * u + li, kfirst), klast);
-            const int lb = a.bs_shift >= 0 ? key >> a.bs_shift : key / bs;
-            src.base[u] = gbase + pt.get<kLds>(lb) * a.k_sb + (int64_t)(key - lb * bs) * a.k_ss;
         }
+    } else {
+        const int key = min(max(kb + (lane & 31), kfirst), klast);
+        const int lb = a.bs_shift >= 0 ? key >> a.bs_shift : key / bs;
+        src.base[0] = gbase + pt.get<kLds>(lb) * a.k_sb + (int64_t)(key - lb * bs) * a.k_ss;
+        src.base[1] = src.base[0];
     }
     return src;
 }
 
-__device__ __forceinline__ uint4_t ld16(const int8_t* p) { return *reinterpret_cast<const uint4_t*>(p); }
+// 16-byte HBM -> LDS copies: LDS[dst + 16 * lane] = global[...]. Issued through asm so the
+// compiler adds no vmcnt wait of its own before the LDS reads; completion is awaited with
+// wait_vm. dma16_s: uniform base + per-lane 32-bit offset; dma16_v: per-lane address + imm.
+__device__ __forceinline__ void dma16_s(const int8_t* sbase, unsigned voff, unsigned m0) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0)
+                 : "memory", "m0");
+}
+// The immediate offset applies to the LDS destination too: the copy lands at m0 + kImm +
+// 16 * lane, so m0 is passed already reduced by kImm.
+template <int kImm>
+__device__ __forceinline__ void dma16_v(const int8_t* vaddr, unsigned lds_dst) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off offset:%2" ::"v"(vaddr), "s"(lds_dst - kImm),
+                 "i"(kImm)
+                 : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// V half (and tail) of a tile: 9 loads of 16 bytes per lane.
-__device__ __forceinline__ void load_v(const TileSrc& src, unsigned lane_off, unsigned tail_off, int lane,
-                                       TileRegs& r) {
+// Per-lane constants of the DMA addressing (see the slot layout).
+struct DmaLane {
+    unsigned kvo, vvo;   // kFast: offsets of this lane's K / V source bytes from its block's base
+    unsigned toff;       // kFast: offset of this lane's tail row from its key block's base
+    int tsel;            // key block of this lane's tail row
+    unsigned kb2[4];     // kFast: 4 q k_ss, q = 0..3 (K blocks: rows 4 (i & 3) + q)
+};
+
+// The 17 DMAs of one tile into the slot at LDS address `slot` (8 K blocks, 8 V blocks, tail).
+template <bool kFast>
+__device__ __forceinline__ void issue_tile(const PartialParams& a, const TileSrc& src, const DmaLane& d,
+                                           unsigned slot, int lane) {
+    if constexpr (kFast) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+        for (int i = 0; i < 8; ++i) {
+            const int8_t* kb = src.base[i >> 2] + (int64_t)(4 * (i & 3)) * a.k_ss;
+            dma16_s(kb, d.kvo, slot + kImgK + i * kBlk);
+        }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) r.v[u][c] = ld16(src.base[u] + lane_off + 256 + 64 * c);
-    // row 16 u + li with u = bit 4 of the lane: select the base arithmetically (an indexed
-    // select of src.base would go through scratch)
-    const int64_t delta = src.base[1] - src.base[0];
-    const int64_t pick = -(int64_t)((lane >> 4) & 1);
-    r.t = ld16(src.base[0] + (delta & pick) + tail_off);
+        for (int i = 0; i < 8; ++i) {
+            const int8_t* vb = src.base[i >> 2] + (int64_t)(i & 3) * a.k_ss;
+            dma16_s(vb, d.vvo, slot + kImgV + i * kBlk);
+        }
+        const int64_t delta = src.base[1] - src.base[0];
+        dma16_v<0>(src.base[0] + (delta & -(int64_t)d.tsel) + d.toff, slot + kImgT);
+    } else {
+        // chunk-major images: lanes 0-31 copy chunk 2 i of rows 0..31, lanes 32-63 chunk 2 i + 1
+        const int8_t* row = src.base[0];  // tile row lane & 31
+        const int8_t* p = row + 16 * (lane >> 5);
+        dma16_v<0>(p, slot + kImgK + 0 * 1024);
+        dma16_v<32>(p, slot + kImgK + 1 * 1024);
+        dma16_v<64>(p, slot + kImgK + 2 * 1024);
+        dma16_v<96>(p, slot + kImgK + 3 * 1024);
+        dma16_v<128>(p, slot + kImgK + 4 * 1024);
+        dma16_v<160>(p, slot + kImgK + 5 * 1024);
+        dma16_v<192>(p, slot + kImgK + 6 * 1024);
+        dma16_v<224>(p, slot + kImgK + 7 * 1024);
+        dma16_v<256>(p, slot + kImgV + 0 * 1024);
+        dma16_v<288>(p, slot + kImgV + 1 * 1024);
+        dma16_v<320>(p, slot + kImgV + 2 * 1024);
+        dma16_v<352>(p, slot + kImgV + 3 * 1024);
+        dma16_v<384>(p, slot + kImgV + 4 * 1024);
+        dma16_v<416>(p, slot + kImgV + 5 * 1024);
+        dma16_v<448>(p, slot + kImgV + 6 * 1024);
+        dma16_v<480>(p, slot + kImgV + 7 * 1024);
+        dma16_v<504>(row, slot + kImgT);
+    }
 }
 
-// K half of a tile: 8 loads of 16 bytes per lane, straight into the MFMA operand layout.
-__device__ __forceinline__ void load_k(const TileSrc& src, unsigned lane_off, TileRegs& r) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) r.k[u][c] = ld16(src.base[u] + lane_off + 64 * c);
-}
+// The operands of one tile, read from its LDS slot.
+struct TileOps {
+    uint4_t k[4][2];  // K operand: row 16 u + li, source chunk 4 c + lg
+    int2_t v[17];     // transposed V reads, one per 16-dim block
+    float ks[8];      // k_scale of this lane's keys 16 u + 4 lg + j
+    float vs[8];      // v_scale of the same keys
+};
 
 // One workgroup = kWaves independent waves. Wave w of split s streams tiles tb + w, tb + w + 4,
 // ... of the split and computes all R query rows of the kv head for each (NRB row blocks of
-// 16), so every K/V byte is loaded and widened once. Loads run one tile ahead in registers:
-// tile n + 1 is issued as soon as tile n's registers are free (its V half once written to LDS,
-// its K half once S is computed), so every wave keeps a tile in flight while it computes.
+// 16), so every K/V byte is loaded and widened once. Each wave double-buffers its tiles in LDS:
+// tile n + 1 is copied while tile n is computed, and tile n + 2 is issued as soon as tile n is
+// done, so while the wave waits it has two tiles in flight.
 template <int NRB, bool kFast>
 __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialParams a) {
     constexpr int kLdsWaves = kWaves * kWaveLds;
-    constexpr int kLdsMerge = kWaves * 16 * kOPitch * 4;  // one row block of every wave, aliases the images
+    constexpr int kMergeRows = NRB <= 2 ? 16 * NRB : 16;  // rows merged per round
+    constexpr int kLdsMerge = kWaves * kMergeRows * kOPitch * 4;
     constexpr int kLdsMain = kLdsWaves > kLdsMerge ? kLdsWaves : kLdsMerge;
     constexpr int kLdsStats = kLdsMain;                   // m, l: [wave][NRB][16]
     constexpr int kLdsBt = kLdsStats + 2 * kWaves * NRB * 16 * 4;
@@ -307,10 +359,37 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         return;
     }
 
+    const int nt = max(0, (te - tb - w + kWaves - 1) / kWaves);  // tiles of this wave
+    auto tile_of = [&](int n) { return tb + w + kWaves * n; };
+
+    lds_u8* L = (lds_u8*)lds;
+    const unsigned lds_base = (unsigned)(uintptr_t)L;
+    const unsigned wslots = lds_base + (unsigned)(w * kWaveLds);  // this wave's two slots
+    const int8_t* gbase = a.kc + (int64_t)g * a.k_sh;
+
+    DmaLane dl;
+    {
+        const int qq = l >> 4, c16 = l & 15, p = l & 31;
+        dl.kvo = (unsigned)(qq * a.k_ss) + 16u * (unsigned)(c16 ^ (4 * qq));
+        dl.vvo = (unsigned)(4 * qq * a.k_ss) + 256u + 16u * (unsigned)(c16 ^ (8 * (qq & 1)));
+        const int rr = p < 16 ? p : ((p - 16) ^ 8);  // row inside its key block of tail position p
+        dl.toff = kFast ? (unsigned)(rr * a.k_ss) + 504u : 0u;
+        dl.tsel = p >> 4;
+    }
+
+    // The block table is read-only for the kernel's lifetime: read it through the constant
+    // address space so uniform lookups become scalar loads.
+    const_int_ptr bt_row = (const_int_ptr)(uintptr_t)(a.block_table + (int64_t)b * a.bt_stride);
+    PageTable pt;
+    pt.glob = bt_row;
+    pt.lds = (const lds_int*)(L + kLdsBt);
+    pt.rows16 = (const lds_ull2*)(L + kLdsBt);
+    pt.pfirst = max(tb * kTile, lo) / a.block_size;
+
     // ---- Q^T operand (B of S^T = K Q^T) of every row block; lane (lg, li) holds row 16 rb + li,
     //      dims 64 (st / 2) + 16 lg + 8 (st % 2) + [0, 8) in qop[rb][st] ----
     half8_t qop[NRB][8];
-    float qcorr[NRB];
+    float4_t qneg[NRB];  // -1152 sum_d q_d of the row (every element): the widening bias of K
     bool rvalid[NRB];
     int rpos[NRB];
 #pragma unroll
@@ -319,7 +398,6 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         rvalid[rb] = r < R;
         const int qi = r / G, qh = r - (r / G) * G;
         rpos[rb] = ctx0 + qi;
-        float qs = 0.f;
         const _Float16* qrow =
             a.q + (int64_t)(q0 + (rvalid[rb] ? qi : 0)) * a.q_st + (int64_t)(g * G + (rvalid[rb] ? qh : 0)) * kDim;
 #pragma unroll
@@ -328,11 +406,9 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
             const int dim = 64 * (st >> 1) + 16 * lg + 8 * (st & 1);
             __builtin_memcpy(&v, __builtin_assume_aligned(qrow + dim, 4), 16);
             qop[rb][st] = rvalid[rb] ? v : (half8_t)(_Float16)0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qs += (float)qop[rb][st][e];
         }
-        qcorr[rb] = kWidenBias * xor_sum(xor_sum(qs, 16), 32);  // widening bias of K, per row
     }
+    asm volatile("" ::: "memory");  // every Q load is issued before the block table is read
 
     // Running state per row block: max (log2 units), this lane's partial sum of p, and O^T in
     // 17 blocks of 16 "dims" (block m < 16: dims 16 m - 4 .. 16 m + 11; block 16: dims 244..255,
@@ -347,30 +423,9 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         for (int m = 0; m < 17; ++m) oacc[rb][m] = (float4_t)0.f;
     }
 
-    lds_u8* L = (lds_u8*)lds;
-    lds_u8* V = L + w * kWaveLds;  // this wave's V image
-    lds_float* KS = (lds_float*)(V + kScalesOfs);
-    lds_float* VS = KS + kTile;
-    // transposed V reads: lane pair (2 i, 2 i + 1) of a 16-lane group names tile row tkey
-    const int tslot = li >> 1;
-    const int tkey = tslot < 4 ? 4 * lg + tslot : 16 + 4 * lg + (tslot - 4);
-    const int vt_ofs = vrow(tkey) + 8 * (li & 1);
-
-    const int8_t* gbase = a.kc + (int64_t)g * a.k_sh;
-    const unsigned row_off = kFast ? (unsigned)(li * a.k_ss) : 0u;
-    const unsigned lane_off = row_off + 16u * (unsigned)lg;
-    const unsigned tail_off = row_off + 504u;
-
-    // The block table is read-only for the kernel's lifetime: read it through the constant
-    // address space so uniform lookups become scalar loads.
-    const_int_ptr bt_row = (const_int_ptr)(uintptr_t)(a.block_table + (int64_t)b * a.bt_stride);
-    PageTable pt;
-    pt.glob = bt_row;
+    // ---- block-table slice of the split into LDS ----
     {
         const int pk_first = max(tb * kTile, lo), pk_last = min(te * kTile, hi) - 1;
-        pt.pfirst = pk_first / a.block_size;
-        pt.lds = (const lds_int*)(L + kLdsBt);
-        pt.rows16 = (const lds_ull2*)(L + kLdsBt);
         const int* bt_glob = a.block_table + (int64_t)b * a.bt_stride;
         if constexpr (kFast) {
             // byte offset (from this kv head's base) of the first row of every 16-key block of
@@ -397,61 +452,75 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         }
         __syncthreads();
     }
-
-    const int nt = max(0, (te - tb - w + kWaves - 1) / kWaves);  // tiles of this wave
-    auto tile_of = [&](int n) { return tb + w + kWaves * n; };
-
-    // ---- tile n's V half and scales into the LDS image ----
-    auto store_v = [&](const TileRegs& r) __attribute__((always_inline)) {
+    {
+        const half8_t nb = (half8_t)(_Float16)(-kWidenBias);
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int rb = 0; rb < NRB; ++rb) {
+            float4_t acc = (float4_t)0.f;
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                *(lds_uint4*)(V + (4 * c + lg) * kVPitch + vrow(16 * u + li)) = r.v[u][c];
-        // (vector elements are copied to scalars before __builtin_bit_cast: clang lowers a bit
-        // cast of a vector-element lvalue to a load from the vector's first element)
-        if (lg == 0) {
-            const unsigned k0 = r.v[0][0].x, k1 = r.v[1][0].x;
-            KS[li] = __builtin_bit_cast(float, k0);
-            KS[16 + li] = __builtin_bit_cast(float, k1);
+            for (int st = 0; st < 8; ++st) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(nb, qop[rb][st], acc, 0, 0, 0);
+            qneg[rb] = acc;
         }
-        if (l < 32) {
-            const int tr = 16 * (l >> 4) + li;
-            const unsigned vw = r.t.w;
-            VS[tr] = __builtin_bit_cast(float, vw);
-            uint4_t t = r.t;
-            t.w = 0u;  // cleared v_scale bytes: that MFMA output row becomes 1152 * sum P'
-            *(lds_uint4*)(V + 16 * kVPitch + vrow(tr)) = t;
-        }
-    };
+    }
 
-    // ---- S^T = K Q^T for every row block, times k_scale, minus the widening bias; masked
-    //      scores are -inf. Returns whether some row's tile max exceeds its running max + kLazy ----
-    auto tile_scores = [&](int tile, const TileRegs& r, float (&sv)[NRB][8], bool& interior)
-        __attribute__((always_inline)) {
+    // ---- per-lane LDS read offsets inside a slot ----
+    // K operand (u, c): row 16 u + li, source chunk 4 c + lg
+    int kro[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        kro[c] = kFast ? kImgK + (li >> 2) * kBlk + 256 * (li & 3) + 64 * (c ^ (li & 3)) + 16 * lg
+                       : kImgK + (4 * c + lg) * 512 + 16 * li;
+    constexpr int kKroU = kFast ? 4 * kBlk : 256;  // + for key block u = 1
+    // transposed V reads: lane pair (2 i, 2 i + 1) of a 16-lane group names tile row tkey
+    const int tslot = li >> 1;
+    const int tkey = tslot < 4 ? 4 * lg + tslot : 16 + 4 * lg + (tslot - 4);
+    const int th = 8 * (li & 1);
+    // chunk m of row tkey: fast: block (tkey & 3) + 4 (tkey >> 4), slot lg, position m ^ 8 (lg & 1)
+    const int vblk = kImgV + ((tkey & 3) + 4 * (tkey >> 4)) * kBlk + 256 * lg + th;
+    const int vro_lo = kFast ? vblk + ((lg & 1) ? 128 : 0) : kImgV + 16 * tkey + th;   // chunks 0..7
+    const int vro_hi = kFast ? vblk - ((lg & 1) ? 128 : 0) : kImgV + 16 * tkey + th;   // chunks 8..15
+    constexpr int kVroStep = kFast ? 16 : 512;
+    const int tpos = kFast ? (tkey < 16 ? tkey : 16 + ((tkey - 16) ^ 8)) : tkey;
+    const int vro_t = kImgT + 16 * tpos + th;
+    // scales of this lane's keys 16 u + 4 lg + j: k_scale = first word of V chunk 0, v_scale
+    // the last word of the tail
+    int kso[2], vso[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int t0 = 16 * u + 4 * lg;
+        kso[u] = kFast ? kImgV + (4 * u) * kBlk + 256 * lg + ((lg & 1) ? 128 : 0) : kImgV + 16 * t0;
+        const int tp0 = kFast ? (u == 0 ? t0 : 16 + ((t0 - 16) ^ 8)) : t0;
+        vso[u] = kImgT + 16 * tp0 + 12;
+    }
+    constexpr int kKsoStep = kFast ? kBlk : 16;  // + per j
+
+    int tile_cur = tb;  // the tile being computed
+
+    // ---- S^T = K Q^T for every row block (the accumulator starts at -1152 sum q, the widening
+    //      bias of K), times k_scale, relative to the running max: sv = s - m (log2 units; s itself
+    //      while a row has no max yet); masked scores are -inf. Returns whether some row has to
+    //      raise its max: its tile max exceeds the running max by more than kLazy, or it has none ----
+    auto tile_scores = [&](const TileOps& o, float (&sv)[NRB][8], bool& interior) __attribute__((always_inline)) {
         float4_t sacc[NRB][2];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
+            const uint4_t* kr = o.k[c];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
-                    const uint4_t kr = r.k[u][c];
-                    const half8_t kf = hh == 0 ? widen_i8x8(kr.x, kr.y) : widen_i8x8(kr.z, kr.w);
+                    const half8_t kf = hh == 0 ? widen_i8x8(kr[u].x, kr[u].y) : widen_i8x8(kr[u].z, kr[u].w);
 #pragma unroll
                     for (int rb = 0; rb < NRB; ++rb)
                         sacc[rb][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            kf, qop[rb][2 * c + hh], (c | hh) ? sacc[rb][u] : (float4_t)0.f, 0, 0, 0);
+                            kf, qop[rb][2 * c + hh], (c | hh) ? sacc[rb][u] : qneg[rb], 0, 0, 0);
                 }
             }
-            __builtin_amdgcn_sched_barrier(0);  // bounds the operands widened ahead of their MFMAs
         }
         float ks[8];
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) ks[4 * u + j] = KS[16 * u + 4 * lg + j] * a.scale_log2;
-        const int kb = tile * kTile;
+        for (int e = 0; e < 8; ++e) ks[e] = o.ks[e] * a.scale_log2;
+        const int kb = tile_cur * kTile;
         // Interior tile: every key is visible to every row (padding rows have Q = 0 and are
         // never written out), so no per-element mask is needed.
         interior = kb >= lo && kb + kTile <= hi;
@@ -460,11 +529,13 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         bool need = false;
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) {
+            const bool fresh = m_run[rb] == kNegInf;
+            const float nm = fresh ? 0.f : -m_run[rb];
             float mx = kNegInf;
             if (interior) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    sv[rb][e] = (sacc[rb][e >> 2][e & 3] - qcorr[rb]) * ks[e];
+                    sv[rb][e] = __builtin_fmaf(sacc[rb][e >> 2][e & 3], ks[e], nm);
                     mx = fmaxf(mx, sv[rb][e]);
                 }
             } else {
@@ -474,110 +545,148 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
                     const int rp = rpos[rb];
                     const bool vis = rvalid[rb] & (t >= lo) & (t < hi) & (!a.causal | (t <= rp)) &
                                      ((a.window <= 0) | ((rp - t) < a.window));
-                    sv[rb][e] = vis ? (sacc[rb][e >> 2][e & 3] - qcorr[rb]) * ks[e] : kNegInf;
+                    sv[rb][e] = vis ? __builtin_fmaf(sacc[rb][e >> 2][e & 3], ks[e], nm) : kNegInf;
                     mx = fmaxf(mx, sv[rb][e]);
                 }
             }
-            need |= mx > m_run[rb] + kLazy;
+            need |= fresh ? mx > kNegInf : mx > kLazy;
         }
         return need;
     };
 
-    // rare path: raise the running max of the rows that need it and rescale their state
-    auto raise_max = [&](const float (&sv)[NRB][8]) __attribute__((always_inline)) {
+    // rare path: raise the running max of the rows that need it, shift their relative scores and
+    // rescale their state
+    auto raise_max = [&](float (&sv)[NRB][8]) __attribute__((always_inline)) {
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) {
             float mloc = kNegInf;
 #pragma unroll
             for (int e = 0; e < 8; ++e) mloc = fmaxf(mloc, sv[rb][e]);
-            const float mrow = xor_max(xor_max(mloc, 16), 32);
-            const float m_new = mrow > m_run[rb] + kLazy ? mrow : m_run[rb];
-            const float alpha = m_run[rb] == kNegInf ? 0.f : __builtin_amdgcn_exp2f(m_run[rb] - m_new);
-            m_run[rb] = m_new;
-            l_run[rb] *= alpha;
+            const float mrow = xor_max(xor_max(mloc, 16), 32);  // tile max, relative to m_run
+            const bool fresh = m_run[rb] == kNegInf;
+            const bool raise = fresh ? mrow > kNegInf : mrow > kLazy;
+            const float shift = raise ? mrow : 0.f;
+            const float alpha = fresh ? 0.f : __builtin_amdgcn_exp2f(-shift);
+            if (raise) m_run[rb] = fresh ? mrow : m_run[rb] + mrow;
 #pragma unroll
-            for (int m = 0; m < 17; ++m) oacc[rb][m] *= alpha;
+            for (int e = 0; e < 8; ++e) sv[rb][e] -= shift;
+            l_run[rb] *= alpha;
+            // O is still zero while every row of the block is fresh: skip the rescale then
+            if (__builtin_amdgcn_ballot_w64(!fresh) != 0) {
+#pragma unroll
+                for (int m = 0; m < 17; ++m) oacc[rb][m] *= alpha;
+            }
         }
     };
 
-    // ---- P' = 2^(s - m) * v_scale * 16 as two fp16 parts (hi + lo, ~22 significant bits: a
+    // ---- p = 2^sv; P' = p * v_scale * 16 as two fp16 parts (hi + lo, ~22 significant bits: a
     //      single fp16 would put 2^-12 relative error on every term, too much next to outlier V
-    //      rows), then O^T += V^T hi^T + V^T lo^T for every row block ----
-    auto tile_values = [&](const float (&sv)[NRB][8], bool interior) __attribute__((always_inline)) {
+    //      rows); then O^T += V^T hi^T + V^T lo^T for every row block ----
+    auto tile_values = [&](const TileOps& o, const float (&sv)[NRB][8], bool interior) __attribute__((always_inline)) {
         float vsc[8];
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int e = 0; e < 8; ++e) vsc[e] = o.vs[e] * kPScale;
+        if (!interior) {  // outside [lo, hi) a scale may be garbage or NaN: use 0
 #pragma unroll
-            for (int j = 0; j < 4; ++j) vsc[4 * u + j] = VS[16 * u + 4 * lg + j] * kPScale;
+            for (int e = 0; e < 8; ++e) {
+                const int t = tile_cur * kTile + 16 * (e >> 2) + 4 * lg + (e & 3);
+                vsc[e] = (t >= lo) & (t < hi) ? vsc[e] : 0.f;
+            }
+        }
         half8_t phi[NRB], plo[NRB];
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) {
             float psum = 0.f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                // masked scores are -inf; the select also keeps a NaN scale of a masked row out
-                const bool vis = interior || sv[rb][e] > kNegInf;
-                const float p = vis ? __builtin_amdgcn_exp2f(sv[rb][e] - m_run[rb]) : 0.f;
+                const float p = __builtin_amdgcn_exp2f(sv[rb][e]);  // masked: 2^-inf = 0
                 psum += p;
-                const float pv = vis ? p * vsc[e] : 0.f;
-                const _Float16 h = (_Float16)pv;
+                const _Float16 h = (_Float16)(p * vsc[e]);
                 phi[rb][e] = h;
-                plo[rb][e] = (_Float16)(pv - (float)h);
+                plo[rb][e] = (_Float16)__builtin_fmaf(p, vsc[e], -(float)h);
             }
             l_run[rb] += psum;
         }
 #pragma unroll
         for (int m = 0; m < 17; ++m) {
-            const int2_t raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_int2*)(V + m * kVPitch + vt_ofs));
-            const half8_t vf = widen_i8x8((unsigned)raw.x, (unsigned)raw.y);
+            const half8_t vf = widen_i8x8((unsigned)o.v[m].x, (unsigned)o.v[m].y);
 #pragma unroll
             for (int rb = 0; rb < NRB; ++rb)
                 oacc[rb][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, phi[rb], oacc[rb][m], 0, 0, 0);
 #pragma unroll
             for (int rb = 0; rb < NRB; ++rb)
                 oacc[rb][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, plo[rb], oacc[rb][m], 0, 0, 0);
-            if ((m & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // ---- every operand of a tile from its slot into registers, so the slot can be refilled
+    //      before the tile is computed: v_scale of this lane's keys (then the v_scale words of the
+    //      slot are cleared: that MFMA output row of the tail block becomes 1152 * sum P'), the K
+    //      operand, k_scale, and the 17 transposed V reads ----
+    auto read_ops = [&](lds_u8* T, TileOps& o) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o.vs[4 * u + j] = *(const lds_float*)(T + vso[u] + 16 * j);
+        if (l < 32) *(lds_float*)(T + kImgT + 16 * l + 12) = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) o.k[c][u] = *(const lds_uint4*)(T + kro[c] + u * kKroU);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o.ks[4 * u + j] = *(const lds_float*)(T + kso[u] + j * kKsoStep);
+#pragma unroll
+        for (int m = 0; m < 17; ++m) {
+            const int ofs = m < 8 ? vro_lo + kVroStep * m : (m < 16 ? vro_hi + kVroStep * m : vro_t);
+            o.v[m] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_int2*)(T + ofs));
         }
     };
 
     // ---- the tile stream of this wave ----
     auto tile_loop = [&](auto lds_flag) __attribute__((always_inline)) {
         constexpr bool kLds = decltype(lds_flag)::value;
-        auto src_of = [&](int n) __attribute__((always_inline)) {
-            return tile_src<kFast, kLds>(a, pt, gbase, tile_of(n), tb, lo, hi, li);
+        auto issue = [&](int n) __attribute__((always_inline)) {
+            wait_lds();  // every LDS access to the slot being refilled has completed
+            issue_tile<kFast>(a, tile_src<kFast, kLds>(a, pt, gbase, tile_of(n), tb, lo, hi, l), dl,
+                              wslots + (unsigned)((n & 1) * kSlot), l);
         };
-        TileRegs r;
-        if (nt > 0) {
-            const TileSrc first = src_of(0);
-            load_v(first, lane_off, tail_off, l, r);
-            load_k(first, lane_off, r);
-        }
-        // The fast inner loop never rescales: O stays in the MFMA accumulators, untouched by
-        // the vector ALU. When some row's max must be raised the loop is left, the rows are
-        // rescaled, the tile is finished and the loop resumes with the next tile, whose loads
-        // are already in flight.
+        // The first two tiles: all loads the compiler can see (Q, block table) have been waited
+        // for by now, so no compiler-inserted wait will include these copies.
+        if (nt > 0) issue(0);
+        if (nt > 1) issue(1);
         float sv[NRB][8];
+        TileOps ops;
         bool interior = true;
         int n = 0;
+        // The fast inner loop never rescales: O stays in the MFMA accumulators, untouched by
+        // the vector ALU. When some row's max must be raised the loop is left, the rows are
+        // rescaled, the tile is finished and the loop resumes with the next tile.
         while (n < nt) {
             bool rare = false;
             for (; n < nt; ++n) {
-                const bool more = n + 1 < nt;
-                TileSrc nxt;
-                if (more) nxt = src_of(n + 1);
-                store_v(r);
-                if (more) load_v(nxt, lane_off, tail_off, l, r);  // V of tile n + 1 into the freed registers
-                const bool need = tile_scores(tile_of(n), r, sv, interior);
-                if (more) load_k(nxt, lane_off, r);  // K of tile n + 1, once S of tile n is computed
+                if (n + 1 < nt)
+                    wait_vm<17>();  // tile n has landed; tile n + 1 may still be in flight
+                else
+                    wait_vm<0>();
+                lds_u8* T = L + w * kWaveLds + (n & 1) * kSlot;
+                tile_cur = tile_of(n);
+                read_ops(T, ops);
+                const bool need = tile_scores(ops, sv, interior);
                 if (__builtin_amdgcn_ballot_w64(need) != 0) {
                     rare = true;
                     break;
                 }
-                tile_values(sv, interior);
+                tile_values(ops, sv, interior);
+                // Refill the slot with tile n + 2 once tile n is computed: the issue can stall
+                // while the memory queues are full, and stalling here overlaps the wait below.
+                if (n + 2 < nt) issue(n + 2);
             }
             if (!rare) break;
             raise_max(sv);
-            tile_values(sv, interior);
+            tile_values(ops, sv, interior);
+            if (n + 2 < nt) issue(n + 2);
             ++n;
         }
     };
@@ -599,48 +708,57 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
             wl[(w * NRB + rb) * 16 + li] = l_row;
         }
     }
-    __syncthreads();  // stats visible; every wave is done with its V image (the slab aliases them)
-    float* slab = reinterpret_cast<float*>(lds);  // [wave][16 rows][kOPitch]
-    const int orow = tid >> 4, dq = (tid & 15) * 16;  // merge thread: row, 16 dims
+    __syncthreads();  // stats visible; every wave is done with its slots (the slab aliases them)
+    float* slab = reinterpret_cast<float*>(lds);  // [wave][kMergeRows][kOPitch]
+    constexpr int kRounds = NRB * 16 / kMergeRows;
+    constexpr int kRbPerRound = kMergeRows / 16;
 #pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) {
-        float M = kNegInf;
+    for (int rd = 0; rd < kRounds; ++rd) {
 #pragma unroll
-        for (int v = 0; v < kWaves; ++v) M = fmaxf(M, wm[(v * NRB + rb) * 16 + li]);
-        const float f = m_run[rb] == kNegInf ? 0.f : exp2f(m_run[rb] - M) * (1.0f / kPScale);
-        float* ob = slab + (w * 16 + li) * kOPitch;
+        for (int k = 0; k < kRbPerRound; ++k) {
+            const int rb = rd * kRbPerRound + k;
+            float M = kNegInf;
 #pragma unroll
-        for (int m = 0; m < 17; ++m) {
-            const int d0 = m < 16 ? 16 * m - 4 + 4 * lg : (lg == 2 ? 252 : -1);
-            if (d0 >= 0 && d0 < kDim) *reinterpret_cast<float4_t*>(ob + d0) = (oacc[rb][m] - corr[rb]) * f;
+            for (int v = 0; v < kWaves; ++v) M = fmaxf(M, wm[(v * NRB + rb) * 16 + li]);
+            const float f = m_run[rb] == kNegInf ? 0.f : exp2f(m_run[rb] - M) * (1.0f / kPScale);
+            float* ob = slab + (w * kMergeRows + 16 * k + li) * kOPitch;
+#pragma unroll
+            for (int m = 0; m < 17; ++m) {
+                const int d0 = m < 16 ? 16 * m - 4 + 4 * lg : (lg == 2 ? 252 : -1);
+                if (d0 >= 0 && d0 < kDim) *reinterpret_cast<float4_t*>(ob + d0) = (oacc[rb][m] - corr[rb]) * f;
+            }
         }
         __syncthreads();
-        const int rr = 16 * rb + orow;
-        if (rr < R) {
+        // thread -> (row of the round, 16 * kRbPerRound dims)
+        constexpr int kDimsPerThread = 16 * kRbPerRound;
+        const int orow = tid / (kDim / kDimsPerThread), dq = (tid % (kDim / kDimsPerThread)) * kDimsPerThread;
+        const int rr = rd * kMergeRows + orow;
+        if (orow < kMergeRows && rr < R) {
             float* dst = a.part_o + prow(rr) * kDim + dq;
 #pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
+            for (int q4 = 0; q4 < kDimsPerThread / 4; ++q4) {
                 float4_t acc = (float4_t)0.f;
 #pragma unroll
                 for (int v = 0; v < kWaves; ++v)
-                    acc += *reinterpret_cast<const float4_t*>(slab + (v * 16 + orow) * kOPitch + dq + 4 * q4);
+                    acc += *reinterpret_cast<const float4_t*>(slab + (v * kMergeRows + orow) * kOPitch + dq + 4 * q4);
                 *reinterpret_cast<float4_t*>(dst + 4 * q4) = acc;
             }
             if (dq == 0) {
+                const int rbo = rr >> 4, ro = rr & 15;
                 float Mr = kNegInf;
 #pragma unroll
-                for (int v = 0; v < kWaves; ++v) Mr = fmaxf(Mr, wm[(v * NRB + rb) * 16 + orow]);
+                for (int v = 0; v < kWaves; ++v) Mr = fmaxf(Mr, wm[(v * NRB + rbo) * 16 + ro]);
                 float Lr = 0.f;
 #pragma unroll
                 for (int v = 0; v < kWaves; ++v) {
-                    const float mw = wm[(v * NRB + rb) * 16 + orow];
-                    if (mw != kNegInf) Lr += exp2f(mw - Mr) * wl[(v * NRB + rb) * 16 + orow];
+                    const float mw = wm[(v * NRB + rbo) * 16 + ro];
+                    if (mw != kNegInf) Lr += exp2f(mw - Mr) * wl[(v * NRB + rbo) * 16 + ro];
                 }
                 a.part_m[prow(rr)] = Mr;
                 a.part_l[prow(rr)] = Lr;
             }
         }
-        __syncthreads();  // the slab is rewritten for the next row block
+        if (rd + 1 < kRounds) __syncthreads();  // the slab is rewritten for the next round
     }
 }
 
