@@ -19,6 +19,7 @@
  *   pth_dec_supported_layout   <- supported_layout, kernels/pth_dec/pth_dec.cpp:25-41
  *   pth_dec_decode             <- decode, kernels/pth_dec/pth_dec.cpp:43-91 (the torch op body,
  *                                 with tensors passed as pd_tensor descriptors)
+ *   pth_fa_forward             <- forward_pth, kernels/fa_pth/pth_fa.cpp:41-85 (chunked prefill)
  */
 #ifndef PTH_DEC_H
 #define PTH_DEC_H
@@ -116,6 +117,23 @@ int pth_dec_decode(const pd_tensor* q, const pd_tensor* key_cache, const pd_tens
 
 /* Library version string. */
 const char* pth_dec_version(void);
+
+/*
+ * Causal chunked prefill over the same int8 per-token-head cache. Replaces forward_pth,
+ * kernels/fa_pth/pth_fa.cpp:41-85 (same arguments, meaning and error messages), with the output
+ * passed in instead of allocated:
+ *   q            fp32 [B, Hq, Sq, 256] contiguous; query token i of sequence b sits at absolute
+ *                position q_abs_offset[b] + i and sees keys k <= that position, k < seq_lens[b]
+ *   key_cache / value_cache  the cache views (value_cache = key_cache + 260 bytes)
+ *   block_table  int32 [B, max_blocks]; seq_lens, q_abs_offset int32 [B]
+ *   out          fp32 [B, Sq, Hq, 256], unit dim stride
+ * Q is rounded to fp16 for the matrix cores; scores and P.V accumulate in fp32. Returns 0, 1
+ * (validation failure, message in err) or 2 (launch failure).
+ */
+int pth_fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_tensor* value_cache,
+                   const pd_tensor* block_table, const pd_tensor* seq_lens, double scale,
+                   const pd_tensor* q_abs_offset, const pd_tensor* out, hipStream_t stream, char* err,
+                   int errlen);
 
 #ifdef __cplusplus
 }

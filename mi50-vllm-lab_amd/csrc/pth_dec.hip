@@ -195,8 +195,8 @@ struct TileSrc {
     const int8_t* base[2];
 };
 
-template <bool kFast, bool kLds>
-__device__ __forceinline__ TileSrc tile_src(const PartialParams& a, const PageTable& pt, const int8_t* gbase,
+template <bool kFast, bool kLds, class P>
+__device__ __forceinline__ TileSrc tile_src(const P& a, const PageTable& pt, const int8_t* gbase,
                                             int tile, int tb, int lo, int hi, int lane) {
     if constexpr (kFast && kLds) {
         // precomputed when the split started: one LDS read, no address arithmetic. The halves
@@ -261,8 +261,8 @@ struct DmaLane {
 };
 
 // The 17 DMAs of one tile into the slot at LDS address `slot` (8 K blocks, 8 V blocks, tail).
-template <bool kFast>
-__device__ __forceinline__ void issue_tile(const PartialParams& a, const TileSrc& src, const DmaLane& d,
+template <bool kFast, class P>
+__device__ __forceinline__ void issue_tile(const P& a, const TileSrc& src, const DmaLane& d,
                                            unsigned slot, int lane) {
     if constexpr (kFast) {
 #pragma unroll
@@ -862,6 +862,399 @@ __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) 
 }
 
 // ---------------------------------------------------------------------------------------
+// Chunked prefill over the same cache (kernels/fa_pth/pth_fa.cpp:41-85 interface): causal
+// attention of Sq query tokens per sequence, query token i at absolute position q_abs + i,
+// against keys [0, seq_len). One workgroup takes kFaTok query tokens of one sequence and all G
+// heads of one kv head (kFaRows = 192 rows, 48 per wave as 3 row blocks of 16), streams every
+// visible 32-key tile once through a 4-slot LDS ring shared by its 4 waves (wave 0 issues the
+// copies, 3 tiles ahead), and computes S^T = K Q^T and O^T += V^T P^T on fp16 MFMA with fp32
+// accumulation, as the decode kernel does. There is no split: each row is normalised in
+// registers and stored once. Q arrives as fp32 and is rounded to fp16 for the MFMA.
+constexpr int kFaWaves = 4;
+constexpr int kFaRB = 3;                        // row blocks per wave
+constexpr int kFaRows = kFaWaves * kFaRB * 16;  // 192
+constexpr int kFaSlots = 4;
+constexpr int kFaQReg = 8;                      // 32-dim steps of Q held in registers
+constexpr int kFaQLds = 8 - kFaQReg;            // 32-dim steps of Q read from LDS for every tile
+constexpr int kFaQHi = kFaWaves * kFaRB * kFaQLds * 1024;
+constexpr int kFaBt = 5120;                     // 16-key blocks of the block-table table in LDS
+
+struct FaParams {
+    const float* q;
+    int64_t q_sb, q_sh, q_st;  // elements between batches / heads / tokens of q [B, Hq, Sq, 256]
+    const int8_t* kc;
+    int64_t k_sb, k_ss, k_sh;
+    const int* block_table;
+    int64_t bt_stride;
+    const int* seq_lens;
+    const int* q_abs;
+    float* out;
+    int64_t o_sb, o_st, o_sh;  // elements between batches / tokens / heads of out [B, Sq, Hq, 256]
+    int Sq, Hq, G, tok_per_wg, block_size, bs_shift;
+    float scale_log2;
+};
+
+template <bool kFast>
+__global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaParams a) {
+    constexpr int kLdsSlots = kFaSlots * kSlot;
+    constexpr int kLdsQ = kLdsSlots;
+    constexpr int kLdsBt = kLdsQ + kFaQHi;
+    constexpr int kLdsBytes = kLdsBt + kFaBt * 8;
+    static_assert(kLdsBytes <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+
+    const int qt = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, l = tid & 63, lg = l >> 4, li = l & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = a.G;
+    const int tq0 = qt * a.tok_per_wg;                 // first query token of the workgroup
+    const int ntok = min(a.tok_per_wg, a.Sq - tq0);    // query tokens of the workgroup
+    const int seq_len = a.seq_lens[b];
+    const int qabs = a.q_abs[b];
+    // keys any row can see: [0, min(seq_len, last row's position + 1))
+    const int hi = min(seq_len, qabs + tq0 + ntok);
+    const int ntiles = hi > 0 ? (hi - 1) / kTile + 1 : 0;
+    const int pmin = qabs + tq0;                       // smallest row position
+
+    // ---- rows of this wave: row r = 48 w + 16 rb + li -> (token r / G, head r % G) ----
+    lds_u8* L = (lds_u8*)lds;
+    // Q as fp16 MFMA operands: dims 0..127 stay in registers, dims 128..255 go to LDS (1 KiB per
+    // (row block, 32-dim step), lane-contiguous) and are read back for every tile
+    half8_t qop[kFaRB][kFaQReg];
+    lds_u8* const qhi = L + kLdsQ + w * (kFaRB * kFaQLds * 1024) + 16 * l;
+    float qneg[kFaRB];  // -1152 * sum_d q[row, d]: the K widening bias, the same for every key
+    bool rvalid[kFaRB];
+    int rpos[kFaRB];
+#pragma unroll
+    for (int rb = 0; rb < kFaRB; ++rb) {
+        const int r = 48 * w + 16 * rb + li;
+        const int tok = r / G, hh = r - (r / G) * G;
+        rvalid[rb] = tok < ntok && r < a.tok_per_wg * G;
+        rpos[rb] = qabs + tq0 + tok;
+        const float* qrow = a.q + (int64_t)b * a.q_sb + (int64_t)(g * G + (rvalid[rb] ? hh : 0)) * a.q_sh +
+                            (int64_t)(tq0 + (rvalid[rb] ? tok : 0)) * a.q_st;
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+            const int dim = 64 * (st >> 1) + 16 * lg + 8 * (st & 1);
+            const float4_t x0 = *reinterpret_cast<const float4_t*>(qrow + dim);
+            const float4_t x1 = *reinterpret_cast<const float4_t*>(qrow + dim + 4);
+            const half8_t v = {(_Float16)x0.x, (_Float16)x0.y, (_Float16)x0.z, (_Float16)x0.w,
+                               (_Float16)x1.x, (_Float16)x1.y, (_Float16)x1.z, (_Float16)x1.w};
+            const half8_t qv = rvalid[rb] ? v : (half8_t)(_Float16)0.0f;
+            if (st < kFaQReg)
+                qop[rb][st % kFaQReg] = qv;
+            else
+                *(__attribute__((address_space(3))) half8_t*)(qhi + (kFaQLds * rb + st - kFaQReg) * 1024) = qv;
+        }
+    }
+    asm volatile("" ::: "memory");  // every Q load is issued before the block table is read
+
+    const unsigned lds_base = (unsigned)(uintptr_t)L;
+    const int8_t* gbase = a.kc + (int64_t)g * a.k_sh;
+    DmaLane dl;
+    {
+        const int qq = l >> 4, c16 = l & 15, p = l & 31;
+        dl.kvo = (unsigned)(qq * a.k_ss) + 16u * (unsigned)(c16 ^ (4 * qq));
+        dl.vvo = (unsigned)(4 * qq * a.k_ss) + 256u + 16u * (unsigned)(c16 ^ (8 * (qq & 1)));
+        const int rr = p < 16 ? p : ((p - 16) ^ 8);
+        dl.toff = kFast ? (unsigned)(rr * a.k_ss) + 504u : 0u;
+        dl.tsel = p >> 4;
+    }
+
+    // ---- block table of the workgroup's keys into LDS (row offsets of 16-key blocks, or pages) ----
+    const_int_ptr bt_row = (const_int_ptr)(uintptr_t)(a.block_table + (int64_t)b * a.bt_stride);
+    PageTable pt;
+    pt.glob = bt_row;
+    pt.lds = (const lds_int*)(L + kLdsBt);
+    pt.rows16 = (const lds_ull2*)(L + kLdsBt);
+    pt.pfirst = 0;
+    {
+        const int* bt_glob = a.block_table + (int64_t)b * a.bt_stride;
+        if constexpr (kFast) {
+            const int nblk = 2 * ntiles;
+            pt.in_lds = nblk <= kFaBt;
+            if (pt.in_lds) {
+                lds_u64* dst = (lds_u64*)(L + kLdsBt);
+                for (int i = tid; i < nblk; i += kFaWaves * 64) {
+                    const int kb = (i >> 1) * kTile;
+                    const int klast = min(kb + kTile - 1, hi - 1);
+                    const int key0 = min(kb + 16 * (i & 1), klast) & ~15;
+                    const int lb = key0 / a.block_size;
+                    dst[i] = (uint64_t)((int64_t)bt_glob[lb] * a.k_sb + (int64_t)(key0 - lb * a.block_size) * a.k_ss);
+                }
+            }
+        } else {
+            const int npages = hi > 0 ? (hi - 1) / a.block_size + 1 : 0;
+            pt.in_lds = npages <= 2 * kFaBt;
+            if (pt.in_lds) {
+                lds_int* dst = (lds_int*)(L + kLdsBt);
+                for (int i = tid; i < npages; i += kFaWaves * 64) dst[i] = bt_glob[i];
+            }
+        }
+        __syncthreads();
+    }
+    {
+        const half8_t nb = (half8_t)(_Float16)(-kWidenBias);
+#pragma unroll
+        for (int rb = 0; rb < kFaRB; ++rb) {
+            float4_t acc = (float4_t)0.f;
+#pragma unroll
+            for (int st = 0; st < 8; ++st)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    nb, st < kFaQReg ? qop[rb][st % kFaQReg]
+                                     : *(__attribute__((address_space(3))) half8_t*)(qhi + (kFaQLds * rb + st - kFaQReg) * 1024),
+                    acc, 0, 0, 0);
+            qneg[rb] = acc.x;
+        }
+    }
+
+    // ---- per-lane LDS read offsets inside a slot (the decode kernel's layout) ----
+    int kro[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        kro[c] = kFast ? kImgK + (li >> 2) * kBlk + 256 * (li & 3) + 64 * (c ^ (li & 3)) + 16 * lg
+                       : kImgK + (4 * c + lg) * 512 + 16 * li;
+    constexpr int kKroU = kFast ? 4 * kBlk : 256;
+    const int tslot = li >> 1;
+    const int tkey = tslot < 4 ? 4 * lg + tslot : 16 + 4 * lg + (tslot - 4);
+    const int th = 8 * (li & 1);
+    const int vblk = kImgV + ((tkey & 3) + 4 * (tkey >> 4)) * kBlk + 256 * lg + th;
+    const int vro_lo = kFast ? vblk + ((lg & 1) ? 128 : 0) : kImgV + 16 * tkey + th;
+    const int vro_hi = kFast ? vblk - ((lg & 1) ? 128 : 0) : kImgV + 16 * tkey + th;
+    constexpr int kVroStep = kFast ? 16 : 512;
+    const int tpos = kFast ? (tkey < 16 ? tkey : 16 + ((tkey - 16) ^ 8)) : tkey;
+    const int vro_t = kImgT + 16 * tpos + th;
+    int kso[2], vso[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int t0 = 16 * u + 4 * lg;
+        kso[u] = kFast ? kImgV + (4 * u) * kBlk + 256 * lg + ((lg & 1) ? 128 : 0) : kImgV + 16 * t0;
+        const int tp0 = kFast ? (u == 0 ? t0 : 16 + ((t0 - 16) ^ 8)) : t0;
+        vso[u] = kImgT + 16 * tp0 + 12;
+    }
+    constexpr int kKsoStep = kFast ? kBlk : 16;
+
+    float m_run[kFaRB], l_run[kFaRB];
+    float4_t oacc[kFaRB][17], cacc[kFaRB];  // cacc: 1152 * sum of P' per row (the V widening bias)
+#pragma unroll
+    for (int rb = 0; rb < kFaRB; ++rb) {
+        m_run[rb] = kNegInf;
+        l_run[rb] = 0.f;
+        cacc[rb] = (float4_t)0.f;
+#pragma unroll
+        for (int m = 0; m < 17; ++m) oacc[rb][m] = (float4_t)0.f;
+    }
+
+    constexpr int kVAhead = 6;  // V operand reads in flight ahead of their MFMAs
+    const half8_t vbias = (half8_t)(_Float16)kWidenBias;
+
+    // ---- front half of a tile: wait for it, refill the ring, read the operands, S^T = K Q^T,
+    //      relative scores; true when some row's running max must be raised ----
+    auto tile_front = [&](const lds_u8* T, int n, float (&sv)[kFaRB][8], float (&vs)[8], int2_t (&vraw)[17])
+        __attribute__((always_inline)) {
+        float ks[8];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                ks[4 * u + j] = *(const lds_float*)(T + kso[u] + j * kKsoStep) * a.scale_log2;
+                vs[4 * u + j] = *(const lds_float*)(T + vso[u] + 16 * j) * kPScale;
+            }
+        // the K operands of step c + 1 are read while step c multiplies
+        float4_t sacc[kFaRB][2];
+        uint4_t kr[2][2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) kr[0][u] = *(const lds_uint4*)(T + kro[0] + u * kKroU);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            if (c < 3) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u) kr[(c + 1) & 1][u] = *(const lds_uint4*)(T + kro[c + 1] + u * kKroU);
+            }
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int st = 2 * c + hh;
+                half8_t qf[kFaRB];
+#pragma unroll
+                for (int rb = 0; rb < kFaRB; ++rb)
+                    qf[rb] = st < kFaQReg ? qop[rb][st % kFaQReg]
+                                          : *(__attribute__((address_space(3))) half8_t*)(qhi + (kFaQLds * rb + st - kFaQReg) * 1024);
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const uint4_t kk = kr[c & 1][u];
+                    const half8_t kf = hh == 0 ? widen_i8x8(kk.x, kk.y) : widen_i8x8(kk.z, kk.w);
+#pragma unroll
+                    for (int rb = 0; rb < kFaRB; ++rb)
+                        sacc[rb][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            kf, qf[rb], (c | hh) ? sacc[rb][u] : (float4_t)qneg[rb], 0, 0, 0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // the first V operands are in flight during the softmax
+#pragma unroll
+        for (int m = 0; m < kVAhead; ++m) {
+            const int ofs = m < 8 ? vro_lo + kVroStep * m : vro_hi + kVroStep * m;
+            vraw[m] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_int2*)(T + ofs));
+        }
+        // keys past the last visible one may hold garbage scales (even NaN): zero their v_scale
+        // so P' is exactly 0 there
+        const int kb = n * kTile;
+        const bool interior = kb + kTile - 1 <= pmin && kb + kTile <= hi;
+        if (!interior) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int t = kb + 16 * (e >> 2) + 4 * lg + (e & 3);
+                vs[e] = t < hi ? vs[e] : 0.f;
+            }
+        }
+        bool need = false;
+#pragma unroll
+        for (int rb = 0; rb < kFaRB; ++rb) {
+            const bool fresh = m_run[rb] == kNegInf;
+            const float nm = fresh ? 0.f : -m_run[rb];
+            float mx = kNegInf;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int t = kb + 16 * (e >> 2) + 4 * lg + (e & 3);
+                const bool vis = interior || (rvalid[rb] & (t < hi) & (t <= rpos[rb]));
+                sv[rb][e] = vis ? __builtin_fmaf(sacc[rb][e >> 2][e & 3], ks[e], nm) : kNegInf;
+                mx = fmaxf(mx, sv[rb][e]);
+            }
+            need |= fresh ? mx > kNegInf : mx > kLazy;
+        }
+        return need;
+    };
+
+    // ---- rare path: raise the running max of the rows that need it, shift their scores, rescale
+    //      their state (O is still zero while every row of a block is fresh: no rescale then) ----
+    auto raise_max = [&](float (&sv)[kFaRB][8]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int rb = 0; rb < kFaRB; ++rb) {
+            float mloc = kNegInf;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mloc = fmaxf(mloc, sv[rb][e]);
+            const float mrow = xor_max(xor_max(mloc, 16), 32);
+            const bool fresh = m_run[rb] == kNegInf;
+            const bool raise = fresh ? mrow > kNegInf : mrow > kLazy;
+            const float shift = raise ? mrow : 0.f;
+            const float alpha = fresh ? 0.f : __builtin_amdgcn_exp2f(-shift);
+            if (raise) m_run[rb] = fresh ? mrow : m_run[rb] + mrow;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sv[rb][e] -= shift;
+            l_run[rb] *= alpha;
+            if (__builtin_amdgcn_ballot_w64(!fresh) != 0) {
+                cacc[rb] *= alpha;
+#pragma unroll
+                for (int m = 0; m < 17; ++m) oacc[rb][m] *= alpha;
+            }
+        }
+    };
+
+    // ---- back half: p = 2^sv, P' = p * v_scale * 16 in fp16, cacc += 1152 P', O^T += V^T P'^T ----
+    auto tile_back = [&](const lds_u8* T, const float (&sv)[kFaRB][8], const float (&vs)[8], int2_t (&vraw)[17])
+        __attribute__((always_inline)) {
+        half8_t pop[kFaRB];
+#pragma unroll
+        for (int rb = 0; rb < kFaRB; ++rb) {
+            float psum = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float p = __builtin_amdgcn_exp2f(sv[rb][e]);
+                psum += p;
+                pop[rb][e] = (_Float16)(p * vs[e]);
+            }
+            l_run[rb] += psum;
+            cacc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vbias, pop[rb], cacc[rb], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int m = 0; m < 17; ++m) {
+            const int mm = m + kVAhead;
+            if (mm < 17) {
+                const int ofs = mm < 8 ? vro_lo + kVroStep * mm : (mm < 16 ? vro_hi + kVroStep * mm : vro_t);
+                vraw[mm] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_int2*)(T + ofs));
+            }
+            const half8_t vf = widen_i8x8((unsigned)vraw[m].x, (unsigned)vraw[m].y);
+#pragma unroll
+            for (int rb = 0; rb < kFaRB; ++rb)
+                oacc[rb][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pop[rb], oacc[rb][m], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    auto tile_loop = [&](auto lds_flag) __attribute__((always_inline)) {
+        constexpr bool kLds = decltype(lds_flag)::value;
+        auto issue = [&](int n) __attribute__((always_inline)) {
+            wait_lds();
+            issue_tile<kFast>(a, tile_src<kFast, kLds>(a, pt, gbase, n, 0, 0, hi, l), dl,
+                              lds_base + (unsigned)((n % kFaSlots) * kSlot), l);
+        };
+        if (w == 0) {
+            for (int n = 0; n < min(ntiles, kFaSlots - 1); ++n) issue(n);
+        }
+        // every wave passes the barrier of every tile once, in the fast loop or before the rare path
+        auto arrive = [&](int n) __attribute__((always_inline)) {
+            if (w == 0) {  // tile n has landed (later tiles may still be in flight)
+                const int later = min(kFaSlots - 2, ntiles - 1 - n);
+                if (later >= 2)
+                    wait_vm<34>();
+                else if (later == 1)
+                    wait_vm<17>();
+                else
+                    wait_vm<0>();
+            }
+            __syncthreads();  // tile n visible to every wave; every wave is done with tile n - 1
+            if (w == 0 && n + kFaSlots - 1 < ntiles) issue(n + kFaSlots - 1);  // into tile n - 1's slot
+        };
+        float sv[kFaRB][8], vs[8];
+        int2_t vraw[17];
+        int n = 0;
+        // The fast inner loop never rescales: O stays in the MFMA accumulators. When some row's
+        // max must be raised the loop is left, the rows are rescaled, the tile is finished and the
+        // loop resumes with the next tile.
+        while (n < ntiles) {
+            bool rare = false;
+            for (; n < ntiles; ++n) {
+                arrive(n);
+                const lds_u8* T = L + (n % kFaSlots) * kSlot;
+                if (__builtin_amdgcn_ballot_w64(tile_front(T, n, sv, vs, vraw)) != 0) {
+                    rare = true;
+                    break;
+                }
+                tile_back(T, sv, vs, vraw);
+            }
+            if (!rare) break;
+            raise_max(sv);
+            tile_back(L + (n % kFaSlots) * kSlot, sv, vs, vraw);
+            ++n;
+        }
+    };
+    if (pt.in_lds)
+        tile_loop(std::true_type{});
+    else
+        tile_loop(std::false_type{});
+
+    // ---- normalise and store: out[b, tq0 + tok, g G + hh, :] ----
+#pragma unroll
+    for (int rb = 0; rb < kFaRB; ++rb) {
+        const float l_row = xor_sum(xor_sum(l_run[rb], 16), 32);
+        const float inv = l_row > 0.f ? 1.f / (l_row * kPScale) : 0.f;
+        const float corr = cacc[rb].x;
+        if (rvalid[rb]) {
+            const int r = 48 * w + 16 * rb + li;
+            const int tok = r / G, hh = r - (r / G) * G;
+            float* orow = a.out + (int64_t)b * a.o_sb + (int64_t)(tq0 + tok) * a.o_st + (int64_t)(g * G + hh) * a.o_sh;
+#pragma unroll
+            for (int m = 0; m < 17; ++m) {
+                const int d0 = m < 16 ? 16 * m - 4 + 4 * lg : (lg == 2 ? 252 : -1);
+                if (d0 >= 0 && d0 < kDim) *reinterpret_cast<float4_t*>(orow + d0) = (oacc[rb][m] - corr) * inv;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
 // host side
 
 struct LaunchArgs {
@@ -1013,6 +1406,15 @@ LaunchArgs make_args(const void* q, int64_t q_st, const void* kc, int64_t k_sb, 
 
 bool is_dtype(const pd_tensor* t, int dt) { return t && t->dtype == dt; }
 
+hipError_t launch_prefill(const FaParams& p, int batch, int heads_kv, hipStream_t stream) {
+    const dim3 grid((p.Sq + p.tok_per_wg - 1) / p.tok_per_wg, heads_kv, batch);
+    if (fast_block_table(p.block_size, p.k_ss))
+        hipLaunchKernelGGL((pd_prefill_kernel<true>), grid, dim3(kFaWaves * 64), 0, stream, p);
+    else
+        hipLaunchKernelGGL((pd_prefill_kernel<false>), grid, dim3(kFaWaves * 64), 0, stream, p);
+    return hipGetLastError();
+}
+
 bool same_rows(const pd_tensor* scale, const pd_tensor* cache, int64_t byte_off) {
     // f32 scale view [blocks, block_size, Hkv] sitting byte_off bytes into each cache row
     const uintptr_t base = reinterpret_cast<uintptr_t>(cache->data);
@@ -1037,6 +1439,8 @@ bool layout_ok(const pd_tensor* kc, const pd_tensor* vc, const pd_tensor* ks, co
 }
 
 bool is_contig(const pd_tensor* t) {
+    for (int i = 0; i < t->ndim; ++i)
+        if (t->sizes[i] == 0) return true;  // an empty tensor is contiguous whatever its strides
     int64_t expect = 1;
     for (int i = t->ndim - 1; i >= 0; --i) {
         if (t->sizes[i] != 1 && t->strides[i] != expect) return false;
@@ -1170,6 +1574,85 @@ int pth_dec_decode(const pd_tensor* q, const pd_tensor* key_cache, const pd_tens
     return 0;
 }
 
-const char* pth_dec_version(void) { return "pth_dec-gfx950 0.1"; }
+int pth_fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_tensor* value_cache,
+                   const pd_tensor* block_table, const pd_tensor* seq_lens, double scale, const pd_tensor* q_abs_offset,
+                   const pd_tensor* out, hipStream_t stream, char* err, int errlen) {
+    if (!q || !key_cache || !value_cache || !block_table || !seq_lens || !q_abs_offset || !out)
+        return fail(err, errlen, "null tensor descriptor");
+    if (!(q->dtype == PD_DTYPE_FP32 && q->ndim == 4 && is_contig(q)))
+        return fail(err, errlen, "q must be contiguous fp32 [B, Hq, Sq, D]");
+    if (!(key_cache->dtype == PD_DTYPE_INT8 && value_cache->dtype == PD_DTYPE_INT8))
+        return fail(err, errlen, "key/value cache views must be int8");
+    if (!(key_cache->ndim == 4 && value_cache->ndim == 4)) return fail(err, errlen, "cache views must be 4D");
+    if (!(key_cache->strides[3] == 1 && value_cache->strides[3] == 1))
+        return fail(err, errlen, "cache rows must be contiguous");
+    if (!(block_table->dtype == PD_DTYPE_INT32 && seq_lens->dtype == PD_DTYPE_INT32 &&
+          q_abs_offset->dtype == PD_DTYPE_INT32))
+        return fail(err, errlen, "block_table/seq_lens/q_abs_offset must be int32");
+    const int64_t B = q->sizes[0], Hq = q->sizes[1], Sq = q->sizes[2], D = q->sizes[3];
+    const int64_t bs = key_cache->sizes[1], Hkv = key_cache->sizes[2];
+    if (D != 256) return fail(err, errlen, "head_dim must be 256 (only instantiation built)");
+    if (!(key_cache->sizes[3] >= D + 4 && value_cache->sizes[3] >= D + 4))
+        return fail(err, errlen, "cache rows must hold D int8 values and a fp32 scale");
+    if (!(Hkv > 0 && Hq % Hkv == 0)) return fail(err, errlen, "heads_q must be a multiple of heads_kv");
+    if (!(block_table->ndim == 2 && block_table->sizes[0] == B && block_table->strides[1] == 1 &&
+          seq_lens->sizes[0] == B && q_abs_offset->sizes[0] == B && is_contig(seq_lens) && is_contig(q_abs_offset)))
+        return fail(err, errlen, "per-sequence tensors must have B rows");
+    const uintptr_t kb = reinterpret_cast<uintptr_t>(key_cache->data);
+    if (!(kb % 8 == 0 && (reinterpret_cast<uintptr_t>(value_cache->data) % 4) == 0 && key_cache->strides[1] % 8 == 0 &&
+          key_cache->strides[2] % 8 == 0 && key_cache->strides[0] % 8 == 0))
+        return fail(err, errlen, "K rows must be 8-byte aligned and V rows 4-byte aligned");
+    // the kernel reads K and V from one 520-byte row: V must be the same rows, 260 bytes in
+    bool same = reinterpret_cast<uintptr_t>(value_cache->data) == kb + 260;
+    for (int i = 0; i < 3; ++i)
+        same = same && value_cache->strides[i] == key_cache->strides[i] && value_cache->sizes[i] == key_cache->sizes[i];
+    if (!same) return fail(err, errlen, "value_cache must view the same cache rows as key_cache, 260 bytes in");
+    if (!(key_cache->strides[0] <= INT32_MAX && key_cache->strides[1] <= INT32_MAX && key_cache->strides[2] <= INT32_MAX))
+        return fail(err, errlen, "cache strides must be below 2^31");
+    const int64_t G = Hq / Hkv;
+    if (G > kFaRows) return fail(err, errlen, "heads_q / heads_kv must be at most 192");
+    if (!(out->dtype == PD_DTYPE_FP32 && out->ndim == 4 && out->sizes[0] == B && out->sizes[1] == Sq &&
+          out->sizes[2] == Hq && out->sizes[3] == D && out->strides[3] == 1))
+        return fail(err, errlen, "out must be fp32 [B, Sq, Hq, D] with unit dim stride");
+    // q rows are read and out rows written as 16-byte vectors
+    if (!((reinterpret_cast<uintptr_t>(q->data) % 16) == 0 && (reinterpret_cast<uintptr_t>(out->data) % 16) == 0 &&
+          out->strides[0] % 4 == 0 && out->strides[1] % 4 == 0 && out->strides[2] % 4 == 0))
+        return fail(err, errlen, "q and out rows must be 16-byte aligned");
+    if (B == 0 || Sq == 0) return 0;
+    FaParams p;
+    p.q = static_cast<const float*>(q->data);
+    p.q_sb = q->strides[0];
+    p.q_sh = q->strides[1];
+    p.q_st = q->strides[2];
+    p.kc = static_cast<const int8_t*>(key_cache->data);
+    p.k_sb = key_cache->strides[0];
+    p.k_ss = key_cache->strides[1];
+    p.k_sh = key_cache->strides[2];
+    p.block_table = static_cast<const int*>(block_table->data);
+    p.bt_stride = block_table->strides[0];
+    p.seq_lens = static_cast<const int*>(seq_lens->data);
+    p.q_abs = static_cast<const int*>(q_abs_offset->data);
+    p.out = static_cast<float*>(const_cast<void*>(out->data));
+    p.o_sb = out->strides[0];
+    p.o_st = out->strides[1];
+    p.o_sh = out->strides[2];
+    p.Sq = (int)Sq;
+    p.Hq = (int)Hq;
+    p.G = (int)G;
+    p.tok_per_wg = (int)(kFaRows / G);
+    p.block_size = (int)bs;
+    p.bs_shift = (bs & (bs - 1)) == 0 ? __builtin_ctz((unsigned)bs) : -1;
+    p.scale_log2 = (float)scale * 1.4426950408889634f;
+    const hipError_t e = launch_prefill(p, (int)B, (int)Hkv, stream);
+    if (e != hipSuccess) {
+        char msg[256];
+        snprintf(msg, sizeof msg, "pth_fa launch failed: %s", hipGetErrorString(e));
+        fail(err, errlen, msg);
+        return 2;
+    }
+    return 0;
+}
+
+const char* pth_dec_version(void) { return "pth_dec-gfx950 0.2"; }
 
 }  // extern "C"

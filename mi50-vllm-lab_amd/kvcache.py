@@ -287,3 +287,24 @@ def algorithmic_flops(case: DecodeCase) -> int:
             lo = max(0, p - case.window + 1) if case.window > 0 else 0
             total += max(0, hi - lo)
     return 4 * HEAD_DIM * G * total * case.cache.num_kv_heads
+
+
+def prefill_query(case: DecodeCase) -> torch.Tensor:
+    """The case's query tokens as the prefill operator takes them: fp32 [B, Hq, Sq, 256] contiguous.
+
+    Every sequence of the case must have the same number of new tokens Sq (kernels/fa_pth/pth_fa.cpp:35).
+    """
+    sq = case.qlens[0] if case.qlens else 0
+    assert all(q == sq for q in case.qlens), "prefill needs the same chunk length for every sequence"
+    B, hq = case.num_seqs, case.num_q_heads
+    return case.q.reshape(B, sq, hq, HEAD_DIM).permute(0, 2, 1, 3).float().contiguous()
+
+
+def prefill_flops(seq_lens, q_abs, sq: int, num_q_heads: int) -> int:
+    """4 * D * Hq * sum over query rows of visible keys: the reference's FLOP count for a chunk
+    (kernels/fa_pth/test_pth.py:128 for q_abs = seq_len - Sq)."""
+    total = 0
+    for seq, qa in zip(seq_lens, q_abs):
+        for i in range(sq):
+            total += max(0, min(int(seq), int(qa) + i + 1))
+    return 4 * HEAD_DIM * num_q_heads * total

@@ -43,6 +43,7 @@ EXPORTED_SYMBOLS = (
     "pth_dec_supported_layout",
     "pth_dec_decode",
     "pth_dec_version",
+    "pth_fa_forward",
 )
 
 
@@ -90,6 +91,8 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.pth_dec_decode.argtypes = [tp] * 9 + [c_double, tp, tp, tp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
                                               ctypes.c_int64, ctypes.c_int64, vp, ctypes.c_char_p, c_int]
     lib.pth_dec_decode.restype = c_int
+    lib.pth_fa_forward.argtypes = [tp] * 5 + [c_double, tp, tp, vp, ctypes.c_char_p, c_int]
+    lib.pth_fa_forward.restype = c_int
     lib.pth_dec_version.argtypes = []
     lib.pth_dec_version.restype = ctypes.c_char_p
     if path is None:
@@ -148,6 +151,32 @@ def decode(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, 
                                 int(window), 1 if causal else 0, ctypes.c_void_p(stream), err, len(err))
     if rc != 0:
         raise RuntimeError(err.value.decode())
+
+
+def forward_pth(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, block_table: torch.Tensor,
+                seq_lens: torch.Tensor, scale: float, q_abs_offset: torch.Tensor,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal chunked prefill over the int8 per-token-head cache; returns fp32 [B, Sq, Hq, 256].
+
+    q: fp32 [B, Hq, Sq, 256] contiguous; query token i of sequence b is at absolute position
+    q_abs_offset[b] + i and attends to keys k <= that position, k < seq_lens[b].
+    Reference: kernels/fa_pth/pth_fa.cpp:41-85 (same arguments; `out` may be passed in).
+    """
+    if not q.is_cuda:
+        raise RuntimeError("q must be contiguous fp32 [B, Hq, Sq, D]")
+    lib = load_library()
+    if out is None:
+        out = torch.empty((q.shape[0], q.shape[2], q.shape[1], q.shape[3]), dtype=torch.float32, device=q.device)
+    descs = [describe(t) for t in (q, key_cache, value_cache, block_table, seq_lens)]
+    qa, od = describe(q_abs_offset), describe(out)
+    err = ctypes.create_string_buffer(256)
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        rc = lib.pth_fa_forward(*[ctypes.byref(x) for x in descs], float(scale), ctypes.byref(qa), ctypes.byref(od),
+                                ctypes.c_void_p(stream), err, len(err))
+    if rc != 0:
+        raise RuntimeError(err.value.decode())
+    return out
 
 
 def _ptr(t: torch.Tensor, ctype):

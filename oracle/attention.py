@@ -22,6 +22,12 @@ Only pages that hold a key some row can see are read: pages wholly outside every
 `paged_decode_loops` is an independent, loop-form restatement (per row, per key, per dim, no
 vectorisation) for tiny inputs; the tests use it to pin `paged_decode`.
 
+`paged_prefill` restates the reference's prefill check (kernels/fa_pth/test_pth.py:71-82, the
+`exact` float64 path) for the forward_pth interface (kernels/fa_pth/pth_fa.cpp:35-41): q is
+[B, Hq, Sq, 256], query row i of sequence b sits at absolute position q_abs_offset[b] + i and
+sees keys k < seq_lens[b] with k <= that position; the output is [B, Sq, Hq, 256].
+`paged_prefill_loops` is its loop-form twin for tiny inputs.
+
 Parity status: pinned by the checks in tests/test_oracle.py (brute force, closed forms,
 torch scaled_dot_product_attention in float64, permutation invariance, the reference's
 windowed-row formula). vLLM's Triton kernel, which the reference also prints, cannot run here:
@@ -101,6 +107,81 @@ def paged_decode(q, key_cache, value_cache, k_scale, v_scale, block_table, seq_l
             out[q0:q0 + nrows, g * G:(g + 1) * G] = o.reshape(nrows, G, D)
         written[q0:q0 + nrows] = True
     return out, written
+
+
+def paged_prefill(q, key_cache, value_cache, k_scale, v_scale, block_table, seq_lens, scale: float,
+                  q_abs_offset, rows=None):
+    """float64 [B, Sq, Hq, 256] outputs and a bool [B, Sq] mask of rows with a visible key.
+
+    rows: optional iterable of query rows to compute (the others stay 0 and unmarked), so that a
+    full-size chunk can be checked on a sample of rows. Rows that see no key (seq_len <= 0 or a
+    position below 0) stay 0 and unmarked.
+    """
+    qn = _np(q)
+    B, Hq, Sq, D = qn.shape
+    Hkv = _np(key_cache).shape[2]
+    G = Hq // Hkv
+    sl, qa, bt = _np(seq_lens), _np(q_abs_offset), _np(block_table)
+    sel = np.arange(Sq) if rows is None else np.asarray(sorted(set(int(r) for r in rows)), dtype=np.int64)
+    out = np.zeros((B, Sq, Hq, D), dtype=np.float64)
+    written = np.zeros((B, Sq), dtype=bool)
+    for b in range(B):
+        seq = int(sl[b])
+        pos = int(qa[b]) + sel
+        hi = min(seq, int(pos.max()) + 1) if sel.size else 0
+        if hi <= 0:
+            continue
+        k, v = gather_dequant(key_cache, value_cache, k_scale, v_scale, bt[b], 0, hi)
+        mask = np.arange(hi)[None, :] <= pos[:, None]            # [rows, keys]; keys < hi <= seq_len
+        live = mask.any(axis=1)
+        for h in range(Hq):
+            g = h // G
+            for r0 in range(0, sel.size, 256):                    # bounded score blocks
+                rs = slice(r0, min(r0 + 256, sel.size))
+                s = (qn[b, h, sel[rs]].astype(np.float64) @ np.ascontiguousarray(k[:, g]).T) * scale
+                s = np.where(mask[rs], s, -np.inf)
+                mx = s.max(axis=1, keepdims=True)
+                mx = np.where(np.isfinite(mx), mx, 0.0)
+                p = np.exp(s - mx)
+                tot = p.sum(axis=1, keepdims=True)
+                o = (p @ np.ascontiguousarray(v[:, g])) / np.where(tot > 0, tot, 1.0)
+                out[b, sel[rs], h] = np.where(live[rs, None], o, 0.0)
+        written[b, sel[live]] = True
+    return out, written
+
+
+def paged_prefill_loops(q, key_cache, value_cache, k_scale, v_scale, block_table, seq_lens, scale: float,
+                        q_abs_offset):
+    """Loop-form restatement of paged_prefill for tiny inputs: one key and one dim at a time."""
+    qn = _np(q)
+    kc, vc, ks, vs = _np(key_cache), _np(value_cache), _np(k_scale), _np(v_scale)
+    bt, sl, qa = _np(block_table), _np(seq_lens), _np(q_abs_offset)
+    B, Hq, Sq, D = qn.shape
+    Hkv, bs = kc.shape[2], kc.shape[1]
+    out = [[[[0.0] * D for _ in range(Hq)] for _ in range(Sq)] for _ in range(B)]
+    for b in range(B):
+        for i in range(Sq):
+            p_i = int(qa[b]) + i
+            for h in range(Hq):
+                g = h // (Hq // Hkv)
+                scores, vals = [], []
+                for key in range(int(sl[b])):
+                    if key > p_i:
+                        break
+                    blk, slot = int(bt[b][key // bs]), key % bs
+                    dot = 0.0
+                    for d in range(D):
+                        dot += float(qn[b][h][i][d]) * (float(kc[blk][slot][g][d]) * float(ks[blk][slot][g]))
+                    scores.append(dot * scale)
+                    vals.append([float(vc[blk][slot][g][d]) * float(vs[blk][slot][g]) for d in range(D)])
+                if not scores:
+                    continue
+                mx = max(scores)
+                w = [math.exp(x - mx) for x in scores]
+                tot = sum(w)
+                for d in range(D):
+                    out[b][i][h][d] = sum(wi * vi[d] for wi, vi in zip(w, vals)) / tot
+    return np.array(out, dtype=np.float64)
 
 
 def paged_decode_loops(q, key_cache, value_cache, k_scale, v_scale, block_table, seq_lens, query_start_loc,

@@ -29,7 +29,7 @@ def lib():
 def declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(pth_dec_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(pth_(?:dec|fa)_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_header_symbols_exported(lib):
@@ -163,3 +163,62 @@ def test_python_decode_refuses_host_tensors():
         pth_dec.decode(case.q, c.key_cache, c.value_cache, c.k_scale, c.v_scale, case.block_table, case.seq_lens,
                        case.query_start_loc, torch.empty_like(case.q), case.scale, po, pm, pl, case.num_seqs,
                        case.qmax, 4)
+
+
+def call_prefill(lib, case, *, q=None, out=None, key_cache=None, value_cache=None, bt=None, seq_lens=None,
+                 q_abs=None):
+    q = kvc.prefill_query(case) if q is None else q
+    B, hq, sq = q.shape[0], q.shape[1], q.shape[2]
+    out = torch.empty((B, sq, hq, 256), dtype=torch.float32) if out is None else out
+    c = case.cache
+    q_abs = torch.tensor(case.ctxs, dtype=torch.int32) if q_abs is None else q_abs
+    tensors = (q, c.key_cache if key_cache is None else key_cache, c.value_cache if value_cache is None else value_cache,
+               case.block_table if bt is None else bt, case.seq_lens if seq_lens is None else seq_lens)
+    descs = [pth_dec.describe(t) for t in tensors]
+    qa, od = pth_dec.describe(q_abs), pth_dec.describe(out)
+    err = ctypes.create_string_buffer(256)
+    rc = lib.pth_fa_forward(*[ctypes.byref(x) for x in descs], case.scale, ctypes.byref(qa), ctypes.byref(od), None,
+                            err, len(err))
+    return rc, err.value.decode()
+
+
+def test_prefill_validation_messages(lib):
+    """Messages of forward_pth's checks (kernels/fa_pth/pth_fa.cpp:44-68) and of this boundary's own."""
+    case = make(ctxs=[40, 9], qlens=[3, 3])
+    q = kvc.prefill_query(case)
+    B, hq, sq = q.shape[0], q.shape[1], q.shape[2]
+    kc, vc = case.cache.key_cache, case.cache.value_cache
+    cases = [
+        (dict(q=q.half()), "q must be contiguous fp32 [B, Hq, Sq, D]"),
+        (dict(q=q.transpose(1, 2)), "q must be contiguous fp32 [B, Hq, Sq, D]"),
+        (dict(key_cache=kc.view(torch.uint8)), "key/value cache views must be int8"),
+        (dict(key_cache=kc[0]), "cache views must be 4D"),
+        (dict(bt=case.block_table.long()), "must be int32"),
+        (dict(q_abs=torch.tensor([1, 2], dtype=torch.int64)), "must be int32"),
+        (dict(q=q[..., :128].contiguous(), out=torch.empty((B, sq, hq, 128))), "head_dim must be 256"),
+        (dict(key_cache=kc[..., :200], value_cache=vc[..., :200]), "cache rows must hold D int8 values"),
+        (dict(q=torch.zeros((B, 5, sq, 256)), out=torch.empty((B, sq, 5, 256))), "multiple of heads_kv"),
+        (dict(seq_lens=case.seq_lens[:1]), "per-sequence tensors must have B rows"),
+        (dict(value_cache=kc), "value_cache must view the same cache rows"),
+        (dict(out=torch.empty((B, sq, hq, 256), dtype=torch.float16)), "out must be fp32 [B, Sq, Hq, D]"),
+        (dict(out=torch.empty((B, hq, sq, 256))), "out must be fp32 [B, Sq, Hq, D]"),
+        (dict(out=torch.empty((B * sq * hq * 256 + 1,))[1:].view(B, sq, hq, 256)), "16-byte aligned"),
+    ]
+    for kw, msg in cases:
+        rc, text = call_prefill(lib, case, **kw)
+        assert rc == 1 and msg in text, (list(kw.keys()), rc, text)
+
+
+def test_prefill_empty_chunk_is_noop(lib):
+    case = make(ctxs=[40, 9], qlens=[3, 3])
+    q = kvc.prefill_query(case)[:, :, :0].contiguous()
+    rc, text = call_prefill(lib, case, q=q, out=torch.empty((2, 0, 12, 256)))
+    assert rc == 0, text
+
+
+def test_python_prefill_refuses_host_tensors():
+    case = make(ctxs=[40, 9], qlens=[3, 3])
+    c = case.cache
+    with pytest.raises(RuntimeError):
+        pth_dec.forward_pth(kvc.prefill_query(case), c.key_cache, c.value_cache, case.block_table, case.seq_lens,
+                            case.scale, torch.tensor(case.ctxs, dtype=torch.int32))

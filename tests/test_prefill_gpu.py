@@ -1,0 +1,177 @@
+"""GPU parity of the gfx950 chunked-prefill operator (forward_pth interface) against the float64
+oracle.
+
+Cases follow kernels/fa_pth/test_pth.py:104-106 (its seven (ctx, chunk, layout) cases at block
+size 1584, tolerance max-abs < 2e-2) on the full model's heads (24 q / 4 kv), plus the 2048-token
+chunk over a 61,440-token context at block size 16 checked on sampled rows to the decode
+tolerance (max-abs <= 2e-3, mean-abs <= 2e-4), batches with mixed contexts and chunk offsets,
+the generic (block size not a multiple of 16) and global page-table paths, bit-exact invariance
+to the physical page layout, and HIP-graph replay.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import mi50_vllm_lab_amd.kvcache as kvc
+from mi50_vllm_lab_amd import pth_dec
+from oracle import attention as orc
+
+pytestmark = pytest.mark.gpu
+
+HQ, HKV = 24, 4
+BS_REF = 1584
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def oracle_of(c, q_abs, rows=None):
+    return orc.paged_prefill(kvc.prefill_query(c), c.cache.key_cache, c.cache.value_cache, c.cache.k_scale,
+                             c.cache.v_scale, c.block_table, c.seq_lens, c.scale, torch.tensor(q_abs), rows)
+
+
+def gpu_prefill(d, q_abs):
+    q = kvc.prefill_query(d)
+    out = torch.full((q.shape[0], q.shape[2], q.shape[1], 256), float("nan"), dtype=torch.float32, device="cuda")
+    pth_dec.forward_pth(q, d.cache.key_cache, d.cache.value_cache, d.block_table, d.seq_lens, d.scale,
+                        torch.tensor(q_abs, dtype=torch.int32, device="cuda"), out=out)
+    torch.cuda.synchronize()
+    return out
+
+
+def errors(out, ref, written):
+    o = out.double().cpu().numpy()[written]
+    e = np.abs(o - ref[written])
+    return float(e.max()), float(e.mean())
+
+
+# kernels/fa_pth/test_pth.py:104-105: (ctx, chunk, NHD)
+REF_CASES = [(0, 64, False), (0, 1500, False), (1000, 777, False), (BS_REF * 3 - 5, 2048, False),
+             (5000, 2048, True), (20000, 33, False), (12345, 5, False)]
+
+
+@pytest.mark.parametrize("ctx,n,nhd", REF_CASES, ids=[f"ref{i}" for i in range(len(REF_CASES))])
+def test_reference_cases(ctx, n, nhd):
+    c = kvc.make_case([ctx], [n], num_q_heads=HQ, num_kv_heads=HKV, block_size=BS_REF,
+                      layout="NHD" if nhd else "HND", seed=ctx + n, kv_mode="uniform")
+    say(f"prefill ctx={ctx} chunk={n} nhd={nhd}")
+    out = gpu_prefill(c.to("cuda"), [ctx])
+    rows = None if n <= 800 else list(range(0, 32)) + list(range(n - 32, n)) + list(range(100, n, 97))
+    ref, written = oracle_of(c, [ctx], rows)
+    emax, emean = errors(out, ref, written)
+    say(f"  max-abs {emax:.2e} mean-abs {emean:.2e} |ref| {np.abs(ref[written]).mean():.3f}")
+    assert torch.isfinite(out).all()
+    assert math.isfinite(emax) and emax < 2e-2, (ctx, n, emax)
+    assert emax <= 2e-3 and emean <= 2e-4, (ctx, n, emax, emean)
+
+
+def test_chunk_of_2048_over_61440_cached():
+    c = kvc.make_case([61440], [2048], num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=1005)
+    say("prefill 2048 over 61440, bs 16")
+    out = gpu_prefill(c.to("cuda"), [61440])
+    rng = np.random.default_rng(5)
+    rows = sorted(set([0, 1, 31, 32, 2047] + rng.choice(2048, 27, replace=False).tolist()))
+    ref, written = oracle_of(c, [61440], rows)
+    emax, emean = errors(out, ref, written)
+    say(f"  max-abs {emax:.2e} mean-abs {emean:.2e}")
+    assert torch.isfinite(out).all()
+    assert emax <= 2e-3 and emean <= 2e-4, (emax, emean)
+
+
+@pytest.mark.parametrize("bs,layout", [(16, "HND"), (16, "NHD"), (8, "HND"), (1, "NHD"), (48, "HND")])
+def test_batches_with_chunk_offsets(bs, layout):
+    ctxs, sq = [3000, 0, 517], 70
+    c = kvc.make_case(ctxs, [sq] * 3, num_q_heads=HQ, num_kv_heads=HKV, block_size=bs, layout=layout,
+                      seed=bs * 3 + len(layout))
+    # sequence 0: the chunk ends the sequence; 1: rows before its first key and in the middle;
+    # 2: the chunk starts past the end (every row sees every key)
+    q_abs = [3000, -20, 700]
+    say(f"prefill batch bs={bs} layout={layout}")
+    out = gpu_prefill(c.to("cuda"), q_abs)
+    ref, written = oracle_of(c, q_abs)
+    assert not written[1, :20].any() and written[1, 20:].all()
+    for b in range(3):
+        emax, emean = errors(out[b:b + 1], ref[b:b + 1], written[b:b + 1])
+        say(f"  seq {b}: max-abs {emax:.2e} mean-abs {emean:.2e}")
+        assert emax <= 2e-3 and emean <= 2e-4, (b, emax, emean)
+    assert (out.cpu().numpy()[~written] == 0).all()  # rows that see no key are written as 0
+
+
+def abs_value_case(c):
+    """The case with every V quant replaced by its absolute value. The quantised rows hold
+    [-127, 127]; only unused slots (never read) can hold -128."""
+    cache = kvc.clone_cache(c.cache)
+    v = cache.value_cache[..., :256]
+    v.copy_(v.abs())
+    return kvc.DecodeCase(c.q, cache, c.block_table, c.seq_lens, c.query_start_loc, list(c.ctxs), list(c.qlens),
+                          c.num_q_heads, c.scale)
+
+
+def test_outlier_rows_within_fp16_weight_rounding():
+    """P' = p * v_scale enters the MFMA as fp16: each weight carries at most half an fp16 ulp
+    (2^-12) of relative error, so |err| <= 2^-12 * sum_k p_k |V_k| / l per element; the bound
+    checked is 2e-3 + 2^-11 * that sum (exact, from the oracle on |V|). 1% of the K and V rows
+    are 50x outliers, as in the decode operator's long-context workload."""
+    ctxs, sq = [3000, 517], 70
+    c = kvc.make_case(ctxs, [sq] * 2, num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=41,
+                      outlier_frac=0.01, outlier_mult=50.0)
+    q_abs = [3000, 400]
+    say("prefill outliers")
+    out = gpu_prefill(c.to("cuda"), q_abs)
+    ref, written = oracle_of(c, q_abs)
+    mag, _ = oracle_of(abs_value_case(c), q_abs)
+    err = np.abs(out.double().cpu().numpy() - ref)[written]
+    bound = 2e-3 + 2.0 ** -11 * mag[written]
+    say(f"  max-abs {err.max():.2e} max |ref| {np.abs(ref[written]).max():.1f} worst err/bound {(err / bound).max():.3f}")
+    assert (err <= bound).all()
+
+
+@pytest.mark.parametrize("bs", [16, 8])
+def test_page_table_beyond_lds(bs):
+    # more 16-key blocks (bs 16) or pages (bs 8) than the workgroup's LDS table holds
+    c = kvc.make_case([90000], [40], num_q_heads=HQ, num_kv_heads=HKV, block_size=bs, seed=21 + bs)
+    say(f"prefill global page table bs={bs}")
+    out = gpu_prefill(c.to("cuda"), [90000])
+    ref, written = oracle_of(c, [90000], [0, 13, 39])
+    emax, emean = errors(out, ref, written)
+    say(f"  max-abs {emax:.2e} mean-abs {emean:.2e}")
+    assert emax <= 2e-3 and emean <= 2e-4, (emax, emean)
+
+
+@pytest.mark.parametrize("bs", [16, 1584, 8])
+def test_physical_layout_bit_exact(bs):
+    args = dict(num_q_heads=HQ, num_kv_heads=HKV, block_size=bs, seed=78)
+    a = kvc.make_case([2500, 300], [100, 100], layout="HND", layout_seed=5, **args).to("cuda")
+    b = kvc.make_case([2500, 300], [100, 100], layout="NHD", layout_seed=6, **args).to("cuda")
+    say(f"prefill layout invariance bs {bs}")
+    oa = gpu_prefill(a, [2500, 300])
+    ob = gpu_prefill(b, [2500, 300])
+    assert torch.equal(oa.view(torch.int32), ob.view(torch.int32))
+
+
+def test_hip_graph_capture_and_replay():
+    c = kvc.make_case([5000], [256], num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=31).to("cuda")
+    q = kvc.prefill_query(c)
+    qa = torch.tensor([5000], dtype=torch.int32, device="cuda")
+    ref = gpu_prefill(c, [5000])
+    out = torch.zeros_like(ref)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            pth_dec.forward_pth(q, c.cache.key_cache, c.cache.value_cache, c.block_table, c.seq_lens, c.scale, qa,
+                                out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        say(f"graph replay {i}")
+        assert torch.equal(out.view(torch.int32), ref.view(torch.int32))
