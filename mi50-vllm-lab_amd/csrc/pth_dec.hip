@@ -938,6 +938,7 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
             const int dim = 64 * (st >> 1) + 16 * lg + 8 * (st & 1);
             const float4_t x0 = *reinterpret_cast<const float4_t*>(qrow + dim);
             const float4_t x1 = *reinterpret_cast<const float4_t*>(qrow + dim + 4);
+            // Q is rounded to fp16 unscaled: fp16-valued queries enter the matrix cores exactly
             const half8_t v = {(_Float16)x0.x, (_Float16)x0.y, (_Float16)x0.z, (_Float16)x0.w,
                                (_Float16)x1.x, (_Float16)x1.y, (_Float16)x1.z, (_Float16)x1.w};
             const half8_t qv = rvalid[rb] ? v : (half8_t)(_Float16)0.0f;
@@ -1048,17 +1049,23 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
     constexpr int kVAhead = 6;  // V operand reads in flight ahead of their MFMAs
     const half8_t vbias = (half8_t)(_Float16)kWidenBias;
 
-    // ---- front half of a tile: wait for it, refill the ring, read the operands, S^T = K Q^T,
-    //      relative scores; true when some row's running max must be raised ----
-    auto tile_front = [&](const lds_u8* T, int n, float (&sv)[kFaRB][8], float (&vs)[8], int2_t (&vraw)[17])
-        __attribute__((always_inline)) {
+    // Relative scores carry +kPLog2: p' = 2^(s - m + kPLog2) = 16 p, so P' = p' * v_scale spans the
+    // same fp16 range as in the decode kernel; l accumulates p' and the final 1 / l removes it.
+    constexpr float kPLog2 = 4.0f;
+
+    // ---- front half of a tile: read the operands, S^T = K Q^T, relative scores; true when some
+    //      row's running max must be raised. kMasked: the tile crosses the causal diagonal or
+    //      seq_len (interior tiles are visible to every row and skip all masking) ----
+    auto tile_front = [&](auto masked_flag, const lds_u8* T, int n, float (&sv)[kFaRB][8], float (&vs)[8],
+                          int2_t (&vraw)[17]) __attribute__((always_inline)) {
+        constexpr bool kMasked = decltype(masked_flag)::value;
         float ks[8];
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 ks[4 * u + j] = *(const lds_float*)(T + kso[u] + j * kKsoStep) * a.scale_log2;
-                vs[4 * u + j] = *(const lds_float*)(T + vso[u] + 16 * j) * kPScale;
+                vs[4 * u + j] = *(const lds_float*)(T + vso[u] + 16 * j);
             }
         // the K operands of step c + 1 are read while step c multiplies
         float4_t sacc[kFaRB][2];
@@ -1097,11 +1104,9 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
             const int ofs = m < 8 ? vro_lo + kVroStep * m : vro_hi + kVroStep * m;
             vraw[m] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_int2*)(T + ofs));
         }
-        // keys past the last visible one may hold garbage scales (even NaN): zero their v_scale
-        // so P' is exactly 0 there
         const int kb = n * kTile;
-        const bool interior = kb + kTile - 1 <= pmin && kb + kTile <= hi;
-        if (!interior) {
+        if constexpr (kMasked) {
+            // keys past seq_len may hold garbage scales (even NaN): zero their v_scale so P' is 0
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int t = kb + 16 * (e >> 2) + 4 * lg + (e & 3);
@@ -1112,16 +1117,21 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
 #pragma unroll
         for (int rb = 0; rb < kFaRB; ++rb) {
             const bool fresh = m_run[rb] == kNegInf;
-            const float nm = fresh ? 0.f : -m_run[rb];
+            const float nm = (fresh ? 0.f : -m_run[rb]) + kPLog2;
             float mx = kNegInf;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const int t = kb + 16 * (e >> 2) + 4 * lg + (e & 3);
-                const bool vis = interior || (rvalid[rb] & (t < hi) & (t <= rpos[rb]));
-                sv[rb][e] = vis ? __builtin_fmaf(sacc[rb][e >> 2][e & 3], ks[e], nm) : kNegInf;
+                const float x = __builtin_fmaf(sacc[rb][e >> 2][e & 3], ks[e], nm);
+                if constexpr (kMasked) {
+                    const int t = kb + 16 * (e >> 2) + 4 * lg + (e & 3);
+                    const bool vis = rvalid[rb] & (t < hi) & (t <= rpos[rb]);
+                    sv[rb][e] = vis ? x : kNegInf;
+                } else {
+                    sv[rb][e] = x;
+                }
                 mx = fmaxf(mx, sv[rb][e]);
             }
-            need |= fresh ? mx > kNegInf : mx > kLazy;
+            need |= fresh ? mx > kNegInf : mx > kLazy + kPLog2;
         }
         return need;
     };
@@ -1134,7 +1144,7 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
             float mloc = kNegInf;
 #pragma unroll
             for (int e = 0; e < 8; ++e) mloc = fmaxf(mloc, sv[rb][e]);
-            const float mrow = xor_max(xor_max(mloc, 16), 32);
+            const float mrow = xor_max(xor_max(mloc, 16), 32) - kPLog2;  // tile max relative to m_run
             const bool fresh = m_run[rb] == kNegInf;
             const bool raise = fresh ? mrow > kNegInf : mrow > kLazy;
             const float shift = raise ? mrow : 0.f;
@@ -1151,7 +1161,7 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
         }
     };
 
-    // ---- back half: p = 2^sv, P' = p * v_scale * 16 in fp16, cacc += 1152 P', O^T += V^T P'^T ----
+    // ---- back half: p' = 2^sv, P' = p' * v_scale in fp16, cacc += 1152 P', O^T += V^T P'^T ----
     auto tile_back = [&](const lds_u8* T, const float (&sv)[kFaRB][8], const float (&vs)[8], int2_t (&vraw)[17])
         __attribute__((always_inline)) {
         half8_t pop[kFaRB];
@@ -1183,6 +1193,10 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
         }
     };
 
+    // tiles [0, n_int) are visible to every row of the workgroup: keys below its first row's
+    // position and below hi
+    const int n_int = min(pmin + 1 >= 0 ? (pmin + 1) / kTile : 0, hi / kTile);
+
     auto tile_loop = [&](auto lds_flag) __attribute__((always_inline)) {
         constexpr bool kLds = decltype(lds_flag)::value;
         auto issue = [&](int n) __attribute__((always_inline)) {
@@ -1193,7 +1207,7 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
         if (w == 0) {
             for (int n = 0; n < min(ntiles, kFaSlots - 1); ++n) issue(n);
         }
-        // every wave passes the barrier of every tile once, in the fast loop or before the rare path
+        // every wave passes the barrier of every tile once, in a fast loop or before the rare path
         auto arrive = [&](int n) __attribute__((always_inline)) {
             if (w == 0) {  // tile n has landed (later tiles may still be in flight)
                 const int later = min(kFaSlots - 2, ntiles - 1 - n);
@@ -1209,26 +1223,29 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
         };
         float sv[kFaRB][8], vs[8];
         int2_t vraw[17];
-        int n = 0;
-        // The fast inner loop never rescales: O stays in the MFMA accumulators. When some row's
-        // max must be raised the loop is left, the rows are rescaled, the tile is finished and the
-        // loop resumes with the next tile.
-        while (n < ntiles) {
-            bool rare = false;
-            for (; n < ntiles; ++n) {
-                arrive(n);
-                const lds_u8* T = L + (n % kFaSlots) * kSlot;
-                if (__builtin_amdgcn_ballot_w64(tile_front(T, n, sv, vs, vraw)) != 0) {
-                    rare = true;
-                    break;
+        // The fast inner loops never rescale: O stays in the MFMA accumulators. When some row's
+        // max must be raised the loop is left, the rows are rescaled, the tile is finished and
+        // the loop resumes with the next tile.
+        auto run = [&](auto masked_flag, int n, int n_end) __attribute__((always_inline)) {
+            while (n < n_end) {
+                bool rare = false;
+                for (; n < n_end; ++n) {
+                    arrive(n);
+                    const lds_u8* T = L + (n % kFaSlots) * kSlot;
+                    if (__builtin_amdgcn_ballot_w64(tile_front(masked_flag, T, n, sv, vs, vraw)) != 0) {
+                        rare = true;
+                        break;
+                    }
+                    tile_back(T, sv, vs, vraw);
                 }
-                tile_back(T, sv, vs, vraw);
+                if (!rare) break;
+                raise_max(sv);
+                tile_back(L + (n % kFaSlots) * kSlot, sv, vs, vraw);
+                ++n;
             }
-            if (!rare) break;
-            raise_max(sv);
-            tile_back(L + (n % kFaSlots) * kSlot, sv, vs, vraw);
-            ++n;
-        }
+        };
+        run(std::false_type{}, 0, n_int);
+        run(std::true_type{}, n_int, ntiles);
     };
     if (pt.in_lds)
         tile_loop(std::true_type{});
@@ -1239,7 +1256,7 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
 #pragma unroll
     for (int rb = 0; rb < kFaRB; ++rb) {
         const float l_row = xor_sum(xor_sum(l_run[rb], 16), 32);
-        const float inv = l_row > 0.f ? 1.f / (l_row * kPScale) : 0.f;
+        const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
         const float corr = cacc[rb].x;
         if (rvalid[rb]) {
             const int r = 48 * w + 16 * rb + li;
