@@ -864,20 +864,25 @@ __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) 
 // ---------------------------------------------------------------------------------------
 // Chunked prefill over the same cache (kernels/fa_pth/pth_fa.cpp:41-85 interface): causal
 // attention of Sq query tokens per sequence, query token i at absolute position q_abs + i,
-// against keys [0, seq_len). One workgroup takes kFaTok query tokens of one sequence and all G
-// heads of one kv head (kFaRows = 192 rows, 48 per wave as 3 row blocks of 16), streams every
-// visible 32-key tile once through a 4-slot LDS ring shared by its 4 waves (wave 0 issues the
-// copies, 3 tiles ahead), and computes S^T = K Q^T and O^T += V^T P^T on fp16 MFMA with fp32
-// accumulation, as the decode kernel does. There is no split: each row is normalised in
+// against keys [0, seq_len). One workgroup takes tok_per_wg query tokens of one sequence and all
+// G heads of one kv head (kFaRows = 192 rows, 48 per wave as 3 row blocks of 16) and streams
+// every visible 32-key tile once:
+//   HBM -> LDS   each wave copies a quarter of every tile into a 4-slot ring, 4 tiles ahead;
+//   int8 -> fp16 each wave widens a quarter of tile n + 1 (K operands, transposed V operands,
+//                the tile's scales) into one of two fp16 buffers while it computes tile n;
+//   MFMA         S^T = K Q^T and O^T += V^T P^T on fp16 MFMA with fp32 accumulation, Q held in
+//                registers, K and V operands read from the fp16 buffer.
+// One barrier per tile orders the three stages. There is no split: each row is normalised in
 // registers and stored once. Q arrives as fp32 and is rounded to fp16 for the MFMA.
 constexpr int kFaWaves = 4;
 constexpr int kFaRB = 3;                        // row blocks per wave
 constexpr int kFaRows = kFaWaves * kFaRB * 16;  // 192
-constexpr int kFaSlots = 4;
-constexpr int kFaQReg = 8;                      // 32-dim steps of Q held in registers
-constexpr int kFaQLds = 8 - kFaQReg;            // 32-dim steps of Q read from LDS for every tile
-constexpr int kFaQHi = kFaWaves * kFaRB * kFaQLds * 1024;
-constexpr int kFaBt = 5120;                     // 16-key blocks of the block-table table in LDS
+constexpr int kFaRaw = 4;                       // raw (int8) tile slots
+constexpr int kFaHK = 16 * 1024;                // fp16 K operands: (32-dim step, 16-key block) x 1 KiB
+constexpr int kFaHV = 17 * 1024;                // fp16 V^T operands: 17 16-dim blocks x 1 KiB
+constexpr int kFaHS = 256;                      // k_scale * scale * log2(e) [32], v_scale [32]
+constexpr int kFaHBuf = kFaHK + kFaHV + kFaHS;
+constexpr int kFaBt = 6144;                     // 16-key blocks (or pages) of the LDS block table
 
 struct FaParams {
     const float* q;
@@ -891,15 +896,66 @@ struct FaParams {
     float* out;
     int64_t o_sb, o_st, o_sh;  // elements between batches / tokens / heads of out [B, Sq, Hq, 256]
     int Sq, Hq, G, tok_per_wg, block_size, bs_shift;
+    int bt32;                  // every K row lies within 2^35 bytes of the cache base
     float scale_log2;
 };
 
+// The quarter `part` of a tile's 17 copies: K blocks 2 part, 2 part + 1, V blocks 2 part,
+// 2 part + 1, and the tail for part 3.
+template <bool kFast, int kPart, class P>
+__device__ __forceinline__ void issue_quarter(const P& a, const TileSrc& src, const DmaLane& d, unsigned slot,
+                                              int lane) {
+    if constexpr (kFast) {
+#pragma unroll
+        for (int i = 2 * kPart; i < 2 * kPart + 2; ++i) {
+            const int8_t* kb = src.base[i >> 2] + (int64_t)(4 * (i & 3)) * a.k_ss;
+            dma16_s(kb, d.kvo, slot + kImgK + i * kBlk);
+        }
+#pragma unroll
+        for (int i = 2 * kPart; i < 2 * kPart + 2; ++i) {
+            const int8_t* vb = src.base[i >> 2] + (int64_t)(i & 3) * a.k_ss;
+            dma16_s(vb, d.vvo, slot + kImgV + i * kBlk);
+        }
+        if constexpr (kPart == 3) {
+            const int64_t delta = src.base[1] - src.base[0];
+            dma16_v<0>(src.base[0] + (delta & -(int64_t)d.tsel) + d.toff, slot + kImgT);
+        }
+    } else {
+        const int8_t* row = src.base[0];  // tile row lane & 31
+        const int8_t* p = row + 16 * (lane >> 5);
+        dma16_v<64 * kPart>(p, slot + kImgK + (2 * kPart) * 1024);
+        dma16_v<64 * kPart + 32>(p, slot + kImgK + (2 * kPart + 1) * 1024);
+        dma16_v<256 + 64 * kPart>(p, slot + kImgV + (2 * kPart) * 1024);
+        dma16_v<256 + 64 * kPart + 32>(p, slot + kImgV + (2 * kPart + 1) * 1024);
+        if constexpr (kPart == 3) dma16_v<504>(row, slot + kImgT);
+    }
+}
+
+// Wait until at most `later` tiles' copies of this wave (4 per tile, 5 for wave 3) are in flight.
+__device__ __forceinline__ void wait_quarters(int later, bool tail) {
+    if (tail) {
+        if (later >= 2)
+            wait_vm<10>();
+        else if (later == 1)
+            wait_vm<5>();
+        else
+            wait_vm<0>();
+    } else {
+        if (later >= 2)
+            wait_vm<8>();
+        else if (later == 1)
+            wait_vm<4>();
+        else
+            wait_vm<0>();
+    }
+}
+
 template <bool kFast>
 __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaParams a) {
-    constexpr int kLdsSlots = kFaSlots * kSlot;
-    constexpr int kLdsQ = kLdsSlots;
-    constexpr int kLdsBt = kLdsQ + kFaQHi;
-    constexpr int kLdsBytes = kLdsBt + kFaBt * 8;
+    constexpr int kLdsRaw = 0;
+    constexpr int kLdsH = kLdsRaw + kFaRaw * kSlot;
+    constexpr int kLdsBt = kLdsH + 2 * kFaHBuf;
+    constexpr int kLdsBytes = kLdsBt + kFaBt * 4;
     static_assert(kLdsBytes <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
     __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
 
@@ -917,11 +973,7 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
     const int pmin = qabs + tq0;                       // smallest row position
 
     // ---- rows of this wave: row r = 48 w + 16 rb + li -> (token r / G, head r % G) ----
-    lds_u8* L = (lds_u8*)lds;
-    // Q as fp16 MFMA operands: dims 0..127 stay in registers, dims 128..255 go to LDS (1 KiB per
-    // (row block, 32-dim step), lane-contiguous) and are read back for every tile
-    half8_t qop[kFaRB][kFaQReg];
-    lds_u8* const qhi = L + kLdsQ + w * (kFaRB * kFaQLds * 1024) + 16 * l;
+    half8_t qop[kFaRB][8];
     float qneg[kFaRB];  // -1152 * sum_d q[row, d]: the K widening bias, the same for every key
     bool rvalid[kFaRB];
     int rpos[kFaRB];
@@ -941,15 +993,12 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
             // Q is rounded to fp16 unscaled: fp16-valued queries enter the matrix cores exactly
             const half8_t v = {(_Float16)x0.x, (_Float16)x0.y, (_Float16)x0.z, (_Float16)x0.w,
                                (_Float16)x1.x, (_Float16)x1.y, (_Float16)x1.z, (_Float16)x1.w};
-            const half8_t qv = rvalid[rb] ? v : (half8_t)(_Float16)0.0f;
-            if (st < kFaQReg)
-                qop[rb][st % kFaQReg] = qv;
-            else
-                *(__attribute__((address_space(3))) half8_t*)(qhi + (kFaQLds * rb + st - kFaQReg) * 1024) = qv;
+            qop[rb][st] = rvalid[rb] ? v : (half8_t)(_Float16)0.0f;
         }
     }
     asm volatile("" ::: "memory");  // every Q load is issued before the block table is read
 
+    lds_u8* L = (lds_u8*)lds;
     const unsigned lds_base = (unsigned)(uintptr_t)L;
     const int8_t* gbase = a.kc + (int64_t)g * a.k_sh;
     DmaLane dl;
@@ -962,37 +1011,38 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
         dl.tsel = p >> 4;
     }
 
-    // ---- block table of the workgroup's keys into LDS (row offsets of 16-key blocks, or pages) ----
+    // ---- block table of the workgroup's keys into LDS: for bs % 16 == 0 the byte offset / 8 of
+    //      every 16-key block's first row, else the page numbers ----
     const_int_ptr bt_row = (const_int_ptr)(uintptr_t)(a.block_table + (int64_t)b * a.bt_stride);
     PageTable pt;
     pt.glob = bt_row;
     pt.lds = (const lds_int*)(L + kLdsBt);
-    pt.rows16 = (const lds_ull2*)(L + kLdsBt);
+    pt.rows16 = nullptr;
     pt.pfirst = 0;
     {
         const int* bt_glob = a.block_table + (int64_t)b * a.bt_stride;
         if constexpr (kFast) {
             const int nblk = 2 * ntiles;
-            pt.in_lds = nblk <= kFaBt;
+            pt.in_lds = a.bt32 && nblk <= kFaBt;
             if (pt.in_lds) {
-                lds_u64* dst = (lds_u64*)(L + kLdsBt);
+                lds_int* dst = (lds_int*)(L + kLdsBt);
                 for (int i = tid; i < nblk; i += kFaWaves * 64) {
                     const int kb = (i >> 1) * kTile;
                     const int klast = min(kb + kTile - 1, hi - 1);
                     const int key0 = min(kb + 16 * (i & 1), klast) & ~15;
                     const int lb = key0 / a.block_size;
-                    dst[i] = (uint64_t)((int64_t)bt_glob[lb] * a.k_sb + (int64_t)(key0 - lb * a.block_size) * a.k_ss);
+                    const int64_t off = (int64_t)bt_glob[lb] * a.k_sb + (int64_t)(key0 - lb * a.block_size) * a.k_ss;
+                    dst[i] = (int)(unsigned)((uint64_t)off >> 3);
                 }
             }
         } else {
             const int npages = hi > 0 ? (hi - 1) / a.block_size + 1 : 0;
-            pt.in_lds = npages <= 2 * kFaBt;
+            pt.in_lds = npages <= kFaBt;
             if (pt.in_lds) {
                 lds_int* dst = (lds_int*)(L + kLdsBt);
                 for (int i = tid; i < npages; i += kFaWaves * 64) dst[i] = bt_glob[i];
             }
         }
-        __syncthreads();
     }
     {
         const half8_t nb = (half8_t)(_Float16)(-kWidenBias);
@@ -1000,22 +1050,18 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
         for (int rb = 0; rb < kFaRB; ++rb) {
             float4_t acc = (float4_t)0.f;
 #pragma unroll
-            for (int st = 0; st < 8; ++st)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    nb, st < kFaQReg ? qop[rb][st % kFaQReg]
-                                     : *(__attribute__((address_space(3))) half8_t*)(qhi + (kFaQLds * rb + st - kFaQReg) * 1024),
-                    acc, 0, 0, 0);
+            for (int st = 0; st < 8; ++st) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(nb, qop[rb][st], acc, 0, 0, 0);
             qneg[rb] = acc.x;
         }
     }
+    __syncthreads();  // the LDS block table is complete
 
-    // ---- per-lane LDS read offsets inside a slot (the decode kernel's layout) ----
-    int kro[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-        kro[c] = kFast ? kImgK + (li >> 2) * kBlk + 256 * (li & 3) + 64 * (c ^ (li & 3)) + 16 * lg
-                       : kImgK + (4 * c + lg) * 512 + 16 * li;
+    // ---- this lane's positions in a raw slot (the decode kernel's layout) ----
+    // K operand (32-dim step pair c = this wave's quarter, 16-key block u): 16 source bytes
+    const int kro = kFast ? kImgK + (li >> 2) * kBlk + 256 * (li & 3) + 64 * (w ^ (li & 3)) + 16 * lg
+                          : kImgK + (4 * w + lg) * 512 + 16 * li;
     constexpr int kKroU = kFast ? 4 * kBlk : 256;
+    // transposed V reads: 16-dim block m of this lane's 8 keys
     const int tslot = li >> 1;
     const int tkey = tslot < 4 ? 4 * lg + tslot : 16 + 4 * lg + (tslot - 4);
     const int th = 8 * (li & 1);
@@ -1023,96 +1069,129 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
     const int vro_lo = kFast ? vblk + ((lg & 1) ? 128 : 0) : kImgV + 16 * tkey + th;
     const int vro_hi = kFast ? vblk - ((lg & 1) ? 128 : 0) : kImgV + 16 * tkey + th;
     constexpr int kVroStep = kFast ? 16 : 512;
-    const int tpos = kFast ? (tkey < 16 ? tkey : 16 + ((tkey - 16) ^ 8)) : tkey;
-    const int vro_t = kImgT + 16 * tpos + th;
-    int kso[2], vso[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int t0 = 16 * u + 4 * lg;
-        kso[u] = kFast ? kImgV + (4 * u) * kBlk + 256 * lg + ((lg & 1) ? 128 : 0) : kImgV + 16 * t0;
-        const int tp0 = kFast ? (u == 0 ? t0 : 16 + ((t0 - 16) ^ 8)) : t0;
-        vso[u] = kImgT + 16 * tp0 + 12;
-    }
-    constexpr int kKsoStep = kFast ? kBlk : 16;
+    const int vro_t = kImgT + 16 * (kFast ? (tkey < 16 ? tkey : 16 + ((tkey - 16) ^ 8)) : tkey) + th;
+    // scales of key r = lane (lanes 0..31 of wave 1)
+    const int sr = l & 31, sq = (sr >> 2) & 3;
+    const int kso = kFast ? kImgV + (4 * (sr >> 4) + (sr & 3)) * kBlk + 256 * sq + 128 * (sq & 1) : kImgV + 16 * sr;
+    const int vso = kImgT + 16 * (kFast ? (sr < 16 ? sr : 16 + ((sr - 16) ^ 8)) : sr) + 12;
 
     float m_run[kFaRB], l_run[kFaRB];
-    float4_t oacc[kFaRB][17], cacc[kFaRB];  // cacc: 1152 * sum of P' per row (the V widening bias)
+    float4_t oacc[kFaRB][17];
 #pragma unroll
     for (int rb = 0; rb < kFaRB; ++rb) {
         m_run[rb] = kNegInf;
         l_run[rb] = 0.f;
-        cacc[rb] = (float4_t)0.f;
 #pragma unroll
         for (int m = 0; m < 17; ++m) oacc[rb][m] = (float4_t)0.f;
     }
 
-    constexpr int kVAhead = 6;  // V operand reads in flight ahead of their MFMAs
-    const half8_t vbias = (half8_t)(_Float16)kWidenBias;
+    typedef __attribute__((address_space(3))) half8_t lds_half8;
+    typedef __attribute__((address_space(3))) float4_t lds_float4;
+    auto hbuf = [&](int n) __attribute__((always_inline)) { return L + kLdsH + (n & 1) * kFaHBuf; };
+    auto raw = [&](int n) __attribute__((always_inline)) { return L + kLdsRaw + (n & (kFaRaw - 1)) * kSlot; };
+
+    // ---- widen this wave's quarter of raw tile n into fp16 buffer n & 1: K operands of step
+    //      pair c = w, V^T blocks w, w + 4, w + 8, w + 12 (and 16 for wave 0), the scales (wave 1) ----
+    // ---- widen this wave's quarter of raw tile n into fp16 buffer n & 1: K operands of step
+    //      pair c = w, V^T blocks w, w + 4, w + 8, w + 12 (and 16 for wave 0), the scales (wave 1).
+    //      Staged so that the pieces can be spread between the P.V products of the previous tile ----
+    struct WidenRegs {
+        uint4_t kr[2];
+        int2_t vr[5];
+        float ks, vs;
+    };
+    auto widen_load = [&](int n, WidenRegs& r) __attribute__((always_inline)) {
+        const lds_u8* R = raw(n);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) r.kr[u] = *(const lds_uint4*)(R + kro + u * kKroU);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int m = w + 4 * j;  // wave-uniform
+            const int ofs = (m < 8 ? vro_lo : vro_hi) + kVroStep * m;
+            r.vr[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_int2*)(R + ofs));
+        }
+        r.vr[4] = int2_t{0, 0};
+        if (w == 0) r.vr[4] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_int2*)(R + vro_t));
+        r.ks = 0.f;
+        r.vs = 0.f;
+        if (w == 1) {
+            r.ks = *(const lds_float*)(R + kso) * a.scale_log2;
+            r.vs = *(const lds_float*)(R + vso);
+        }
+    };
+    // piece j of 0..9: K halves 0..3, V blocks 4..7, the tail block 8, the scales 9
+    auto widen_store = [&](int n, const WidenRegs& r, int j) __attribute__((always_inline)) {
+        lds_u8* H = hbuf(n);
+        if (j < 4) {
+            const int u = j >> 1, hh = j & 1;
+            const half8_t kf = hh == 0 ? widen_i8x8(r.kr[u].x, r.kr[u].y) : widen_i8x8(r.kr[u].z, r.kr[u].w);
+            *(lds_half8*)(H + ((2 * w + hh) * 2 + u) * 1024 + 16 * l) = kf;
+        } else if (j < 8) {
+            *(lds_half8*)(H + kFaHK + (w + 4 * (j - 4)) * 1024 + 16 * l) =
+                widen_i8x8((unsigned)r.vr[j - 4].x, (unsigned)r.vr[j - 4].y);
+        } else if (j == 8) {
+            if (w == 0) {
+                // rows 12..15 of the tail block are the v_scale bytes: widened from 0 they are
+                // exactly 1152, so O^T rows 252..255 of that block accumulate 1152 * sum of P'
+                const int2_t vt = li >= 12 ? int2_t{0, 0} : r.vr[4];
+                *(lds_half8*)(H + kFaHK + 16 * 1024 + 16 * l) = widen_i8x8((unsigned)vt.x, (unsigned)vt.y);
+            }
+        } else {
+            if (w == 1 && l < 32) {
+                // keys past seq_len may hold garbage scales (even NaN): v_scale 0 makes P' 0
+                *(lds_float*)(H + kFaHK + kFaHV + 4 * l) = r.ks;
+                *(lds_float*)(H + kFaHK + kFaHV + 128 + 4 * l) = n * kTile + l < hi ? r.vs : 0.f;
+            }
+        }
+    };
+    auto widen = [&](int n) __attribute__((always_inline)) {
+        WidenRegs r;
+        widen_load(n, r);
+#pragma unroll
+        for (int j = 0; j < 10; ++j) widen_store(n, r, j);
+    };
 
     // Relative scores carry +kPLog2: p' = 2^(s - m + kPLog2) = 16 p, so P' = p' * v_scale spans the
     // same fp16 range as in the decode kernel; l accumulates p' and the final 1 / l removes it.
     constexpr float kPLog2 = 4.0f;
 
-    // ---- front half of a tile: read the operands, S^T = K Q^T, relative scores; true when some
-    //      row's running max must be raised. kMasked: the tile crosses the causal diagonal or
-    //      seq_len (interior tiles are visible to every row and skip all masking) ----
-    auto tile_front = [&](auto masked_flag, const lds_u8* T, int n, float (&sv)[kFaRB][8], float (&vs)[8],
-                          int2_t (&vraw)[17]) __attribute__((always_inline)) {
+    // ---- front half of tile n: S^T = K Q^T from fp16 buffer n & 1 (widening tile n + 1 in
+    //      between), relative scores; true when some row's running max must be raised.
+    //      kMasked: the tile crosses the causal diagonal or seq_len ----
+    auto tile_front = [&](auto masked_flag, int n, float (&sv)[kFaRB][8], float (&vs)[8])
+        __attribute__((always_inline)) {
         constexpr bool kMasked = decltype(masked_flag)::value;
+        const lds_u8* H = hbuf(n);
         float ks[8];
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                ks[4 * u + j] = *(const lds_float*)(T + kso[u] + j * kKsoStep) * a.scale_log2;
-                vs[4 * u + j] = *(const lds_float*)(T + vso[u] + 16 * j);
-            }
-        // the K operands of step c + 1 are read while step c multiplies
+        {
+            const float4_t k0 = *(const lds_float4*)(H + kFaHK + kFaHV + 16 * lg);
+            const float4_t k1 = *(const lds_float4*)(H + kFaHK + kFaHV + 64 + 16 * lg);
+            const float4_t v0 = *(const lds_float4*)(H + kFaHK + kFaHV + 128 + 16 * lg);
+            const float4_t v1 = *(const lds_float4*)(H + kFaHK + kFaHV + 192 + 16 * lg);
+            ks[0] = k0.x, ks[1] = k0.y, ks[2] = k0.z, ks[3] = k0.w;
+            ks[4] = k1.x, ks[5] = k1.y, ks[6] = k1.z, ks[7] = k1.w;
+            vs[0] = v0.x, vs[1] = v0.y, vs[2] = v0.z, vs[3] = v0.w;
+            vs[4] = v1.x, vs[5] = v1.y, vs[6] = v1.z, vs[7] = v1.w;
+        }
         float4_t sacc[kFaRB][2];
-        uint4_t kr[2][2];
+        half8_t kf[2][2];  // K operands of 32-dim step st: [st & 1][16-key block u]
+        auto kread = [&](int st, half8_t (&dst)[2]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) kr[0][u] = *(const lds_uint4*)(T + kro[0] + u * kKroU);
+            for (int u = 0; u < 2; ++u) dst[u] = *(const lds_half8*)(H + (2 * st + u) * 1024 + 16 * l);
+        };
+        kread(0, kf[0]);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            if (c < 3) {
+        for (int st = 0; st < 8; ++st) {
+            if (st < 7) kread(st + 1, kf[(st + 1) & 1]);
 #pragma unroll
-                for (int u = 0; u < 2; ++u) kr[(c + 1) & 1][u] = *(const lds_uint4*)(T + kro[c + 1] + u * kKroU);
-            }
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int st = 2 * c + hh;
-                half8_t qf[kFaRB];
+            for (int u = 0; u < 2; ++u)
 #pragma unroll
                 for (int rb = 0; rb < kFaRB; ++rb)
-                    qf[rb] = st < kFaQReg ? qop[rb][st % kFaQReg]
-                                          : *(__attribute__((address_space(3))) half8_t*)(qhi + (kFaQLds * rb + st - kFaQReg) * 1024);
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    const uint4_t kk = kr[c & 1][u];
-                    const half8_t kf = hh == 0 ? widen_i8x8(kk.x, kk.y) : widen_i8x8(kk.z, kk.w);
-#pragma unroll
-                    for (int rb = 0; rb < kFaRB; ++rb)
-                        sacc[rb][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            kf, qf[rb], (c | hh) ? sacc[rb][u] : (float4_t)qneg[rb], 0, 0, 0);
-                }
-            }
+                    sacc[rb][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[st & 1][u], qop[rb][st],
+                                                                         st ? sacc[rb][u] : (float4_t)qneg[rb], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
-        // the first V operands are in flight during the softmax
-#pragma unroll
-        for (int m = 0; m < kVAhead; ++m) {
-            const int ofs = m < 8 ? vro_lo + kVroStep * m : vro_hi + kVroStep * m;
-            vraw[m] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_int2*)(T + ofs));
-        }
         const int kb = n * kTile;
-        if constexpr (kMasked) {
-            // keys past seq_len may hold garbage scales (even NaN): zero their v_scale so P' is 0
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int t = kb + 16 * (e >> 2) + 4 * lg + (e & 3);
-                vs[e] = t < hi ? vs[e] : 0.f;
-            }
-        }
         bool need = false;
 #pragma unroll
         for (int rb = 0; rb < kFaRB; ++rb) {
@@ -1138,7 +1217,11 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
 
     // ---- rare path: raise the running max of the rows that need it, shift their scores, rescale
     //      their state (O is still zero while every row of a block is fresh: no rescale then) ----
-    auto raise_max = [&](float (&sv)[kFaRB][8]) __attribute__((always_inline)) {
+    auto raise_max = [&](float (&sv)[kFaRB][8], int n) __attribute__((always_inline)) {
+        // scratch: this wave's own K blocks of fp16 buffer n + 1, idle until the wave widens
+        // tile n + 1 into them later in this iteration
+        lds_u8* scr = hbuf(n + 1) + 4096 * w + 16 * l;
+        const unsigned scr_addr = (unsigned)(uintptr_t)scr;
 #pragma unroll
         for (int rb = 0; rb < kFaRB; ++rb) {
             float mloc = kNegInf;
@@ -1154,16 +1237,30 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
             for (int e = 0; e < 8; ++e) sv[rb][e] -= shift;
             l_run[rb] *= alpha;
             if (__builtin_amdgcn_ballot_w64(!fresh) != 0) {
-                cacc[rb] *= alpha;
 #pragma unroll
-                for (int m = 0; m < 17; ++m) oacc[rb][m] *= alpha;
+                for (int m = 0; m < 17; ++m) {
+                    float4_t t;
+                    asm volatile("ds_write_b128 %1, %2\n\ts_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+                                 : "=v"(t) : "v"(scr_addr), "a"(oacc[rb][m]) : "memory");
+                    t *= alpha;
+                    asm volatile("ds_write_b128 %1, %2\n\ts_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+                                 : "=a"(oacc[rb][m]) : "v"(scr_addr), "v"(t) : "memory");
+                }
             }
         }
     };
 
-    // ---- back half: p' = 2^sv, P' = p' * v_scale in fp16, cacc += 1152 P', O^T += V^T P'^T ----
-    auto tile_back = [&](const lds_u8* T, const float (&sv)[kFaRB][8], const float (&vs)[8], int2_t (&vraw)[17])
-        __attribute__((always_inline)) {
+    // ---- back half: p' = 2^sv, P' = p' * v_scale in fp16, O^T += V^T P'^T; tile n + 1 is
+    //      widened in pieces between the products ----
+    auto tile_back = [&](int n, const float (&sv)[kFaRB][8], const float (&vs)[8]) __attribute__((always_inline)) {
+        const lds_u8* H = hbuf(n) + kFaHK + 16 * l;
+        const bool wnext = n + 1 < ntiles;
+        WidenRegs wr;
+        if (wnext) widen_load(n + 1, wr);
+        constexpr int kVAhead = 4;  // V operand reads in flight ahead of their MFMAs
+        half8_t vf[17];
+#pragma unroll
+        for (int m = 0; m < kVAhead; ++m) vf[m] = *(const lds_half8*)(H + m * 1024);
         half8_t pop[kFaRB];
 #pragma unroll
         for (int rb = 0; rb < kFaRB; ++rb) {
@@ -1175,20 +1272,15 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
                 pop[rb][e] = (_Float16)(p * vs[e]);
             }
             l_run[rb] += psum;
-            cacc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vbias, pop[rb], cacc[rb], 0, 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int m = 0; m < 17; ++m) {
-            const int mm = m + kVAhead;
-            if (mm < 17) {
-                const int ofs = mm < 8 ? vro_lo + kVroStep * mm : (mm < 16 ? vro_hi + kVroStep * mm : vro_t);
-                vraw[mm] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_int2*)(T + ofs));
-            }
-            const half8_t vf = widen_i8x8((unsigned)vraw[m].x, (unsigned)vraw[m].y);
+            if (m + kVAhead < 17) vf[m + kVAhead] = *(const lds_half8*)(H + (m + kVAhead) * 1024);
 #pragma unroll
             for (int rb = 0; rb < kFaRB; ++rb)
-                oacc[rb][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pop[rb], oacc[rb][m], 0, 0, 0);
+                oacc[rb][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[m], pop[rb], oacc[rb][m], 0, 0, 0);
+            if (m >= 2 && m < 12 && wnext) widen_store(n + 1, wr, m - 2);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -1196,52 +1288,54 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
     // tiles [0, n_int) are visible to every row of the workgroup: keys below its first row's
     // position and below hi
     const int n_int = min(pmin + 1 >= 0 ? (pmin + 1) / kTile : 0, hi / kTile);
+    const bool tail_wave = w == 3;
 
     auto tile_loop = [&](auto lds_flag) __attribute__((always_inline)) {
         constexpr bool kLds = decltype(lds_flag)::value;
         auto issue = [&](int n) __attribute__((always_inline)) {
-            wait_lds();
-            issue_tile<kFast>(a, tile_src<kFast, kLds>(a, pt, gbase, n, 0, 0, hi, l), dl,
-                              lds_base + (unsigned)((n % kFaSlots) * kSlot), l);
-        };
-        if (w == 0) {
-            for (int n = 0; n < min(ntiles, kFaSlots - 1); ++n) issue(n);
-        }
-        // every wave passes the barrier of every tile once, in a fast loop or before the rare path
-        auto arrive = [&](int n) __attribute__((always_inline)) {
-            if (w == 0) {  // tile n has landed (later tiles may still be in flight)
-                const int later = min(kFaSlots - 2, ntiles - 1 - n);
-                if (later >= 2)
-                    wait_vm<34>();
-                else if (later == 1)
-                    wait_vm<17>();
-                else
-                    wait_vm<0>();
+            TileSrc src;
+            if constexpr (kFast && kLds) {
+                const lds_int* e = pt.lds + 2 * n;
+                const unsigned o0 = (unsigned)__builtin_amdgcn_readfirstlane(e[0]);
+                const unsigned o1 = (unsigned)__builtin_amdgcn_readfirstlane(e[1]);
+                src.base[0] = gbase + ((int64_t)o0 << 3);
+                src.base[1] = gbase + ((int64_t)o1 << 3);
+            } else {
+                src = tile_src<kFast, kLds>(a, pt, gbase, n, 0, 0, hi, l);
             }
-            __syncthreads();  // tile n visible to every wave; every wave is done with tile n - 1
-            if (w == 0 && n + kFaSlots - 1 < ntiles) issue(n + kFaSlots - 1);  // into tile n - 1's slot
+            const unsigned slot = lds_base + kLdsRaw + (unsigned)((n & (kFaRaw - 1)) * kSlot);
+            wait_lds();
+            switch (w) {
+                case 0: issue_quarter<kFast, 0>(a, src, dl, slot, l); break;
+                case 1: issue_quarter<kFast, 1>(a, src, dl, slot, l); break;
+                case 2: issue_quarter<kFast, 2>(a, src, dl, slot, l); break;
+                default: issue_quarter<kFast, 3>(a, src, dl, slot, l); break;
+            }
+        };
+        for (int n = 0; n < min(ntiles, kFaRaw); ++n) issue(n);
+        if (ntiles > 0) {
+            // tile 0 has landed; of tiles 1..3 at most 2 are left in flight (conservative)
+            wait_quarters(min(ntiles - 1, 2), tail_wave);
+            __syncthreads();
+            widen(0);
+        }
+        // Iteration n: tile n + 1 has landed and every wave is done with iteration n - 1, so
+        // fp16 buffer n & 1 holds tile n and raw slot n & 3 (widened in iteration n - 1) is free
+        // for tile n + 4.
+        auto arrive = [&](int n) __attribute__((always_inline)) {
+            if (n + 1 < ntiles) wait_quarters(min(2, ntiles - 2 - n), tail_wave);
+            __syncthreads();
+            if (n + kFaRaw < ntiles) issue(n + kFaRaw);
         };
         float sv[kFaRB][8], vs[8];
-        int2_t vraw[17];
         // The fast inner loops never rescale: O stays in the MFMA accumulators. When some row's
         // max must be raised the loop is left, the rows are rescaled, the tile is finished and
         // the loop resumes with the next tile.
-        auto run = [&](auto masked_flag, int n, int n_end) __attribute__((always_inline)) {
-            while (n < n_end) {
-                bool rare = false;
-                for (; n < n_end; ++n) {
-                    arrive(n);
-                    const lds_u8* T = L + (n % kFaSlots) * kSlot;
-                    if (__builtin_amdgcn_ballot_w64(tile_front(masked_flag, T, n, sv, vs, vraw)) != 0) {
-                        rare = true;
-                        break;
-                    }
-                    tile_back(T, sv, vs, vraw);
-                }
-                if (!rare) break;
-                raise_max(sv);
-                tile_back(L + (n % kFaSlots) * kSlot, sv, vs, vraw);
-                ++n;
+        auto run = [&](auto masked_flag, int n0, int n_end) __attribute__((always_inline)) {
+            for (int n = n0; n < n_end; ++n) {
+                arrive(n);
+                if (__builtin_amdgcn_ballot_w64(tile_front(masked_flag, n, sv, vs)) != 0) raise_max(sv, n);
+                tile_back(n, sv, vs);
             }
         };
         run(std::false_type{}, 0, n_int);
@@ -1257,7 +1351,8 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
     for (int rb = 0; rb < kFaRB; ++rb) {
         const float l_row = xor_sum(xor_sum(l_run[rb], 16), 32);
         const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
-        const float corr = cacc[rb].x;
+        const float corr = __shfl(oacc[rb][16].x, 48 + li, 64);  // 1152 * sum of the row's P'
+
         if (rvalid[rb]) {
             const int r = 48 * w + 16 * rb + li;
             const int tok = r / G, hh = r - (r / G) * G;
@@ -1660,6 +1755,11 @@ int pth_fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_tens
     p.block_size = (int)bs;
     p.bs_shift = (bs & (bs - 1)) == 0 ? __builtin_ctz((unsigned)bs) : -1;
     p.scale_log2 = (float)scale * 1.4426950408889634f;
+    // 16-key block offsets fit the LDS table's 32 bits (in 8-byte units) when the cache spans
+    // less than 2^35 bytes
+    const int64_t span = (key_cache->sizes[0] - 1) * key_cache->strides[0] + (bs - 1) * key_cache->strides[1] +
+                         (Hkv - 1) * key_cache->strides[2] + 8;
+    p.bt32 = span < ((int64_t)1 << 35);
     const hipError_t e = launch_prefill(p, (int)B, (int)Hkv, stream);
     if (e != hipSuccess) {
         char msg[256];
