@@ -1070,17 +1070,27 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
     const int vro_hi = kFast ? vblk - ((lg & 1) ? 128 : 0) : kImgV + 16 * tkey + th;
     constexpr int kVroStep = kFast ? 16 : 512;
     const int vro_t = kImgT + 16 * (kFast ? (tkey < 16 ? tkey : 16 + ((tkey - 16) ^ 8)) : tkey) + th;
-    // scales of key r = lane (lanes 0..31 of wave 1)
+    // scales: lane l < 32 reads k_scale of key l, lane l >= 32 v_scale of key l - 32
     const int sr = l & 31, sq = (sr >> 2) & 3;
-    const int kso = kFast ? kImgV + (4 * (sr >> 4) + (sr & 3)) * kBlk + 256 * sq + 128 * (sq & 1) : kImgV + 16 * sr;
-    const int vso = kImgT + 16 * (kFast ? (sr < 16 ? sr : 16 + ((sr - 16) ^ 8)) : sr) + 12;
+    const int sco = l < 32 ? (kFast ? kImgV + (4 * (sr >> 4) + (sr & 3)) * kBlk + 256 * sq + 128 * (sq & 1)
+                                    : kImgV + 16 * sr)
+                           : kImgT + 16 * (kFast ? (sr < 16 ? sr : 16 + ((sr - 16) ^ 8)) : sr) + 12;
+    const float sc_mul = l < 32 ? a.scale_log2 : 1.f;
 
+    // Relative scores carry +kPLog2: p' = 2^(s - m + kPLog2) = 16 p, so P' = p' * v_scale spans the
+    // same fp16 range as in the decode kernel; l accumulates p' and the final 1 / l removes it.
+    constexpr float kPLog2 = 4.0f;
     float m_run[kFaRB], l_run[kFaRB];
+    // per row: the score offset -m_run + kPLog2 (kPLog2 while the row has seen no key) and the
+    // relative score above which m_run must be raised (any finite score while fresh)
+    float nm_run[kFaRB], thr_run[kFaRB];
     float4_t oacc[kFaRB][17];
 #pragma unroll
     for (int rb = 0; rb < kFaRB; ++rb) {
         m_run[rb] = kNegInf;
         l_run[rb] = 0.f;
+        nm_run[rb] = kPLog2;
+        thr_run[rb] = kNegInf;
 #pragma unroll
         for (int m = 0; m < 17; ++m) oacc[rb][m] = (float4_t)0.f;
     }
@@ -1098,7 +1108,7 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
     struct WidenRegs {
         uint4_t kr[2];
         int2_t vr[5];
-        float ks, vs;
+        float sc;
     };
     auto widen_load = [&](int n, WidenRegs& r) __attribute__((always_inline)) {
         const lds_u8* R = raw(n);
@@ -1110,14 +1120,10 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
             const int ofs = (m < 8 ? vro_lo : vro_hi) + kVroStep * m;
             r.vr[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_int2*)(R + ofs));
         }
-        r.vr[4] = int2_t{0, 0};
-        if (w == 0) r.vr[4] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_int2*)(R + vro_t));
-        r.ks = 0.f;
-        r.vs = 0.f;
-        if (w == 1) {
-            r.ks = *(const lds_float*)(R + kso) * a.scale_log2;
-            r.vs = *(const lds_float*)(R + vso);
-        }
+        // every wave reads and writes the tail block and the scales: the copies are identical,
+        // which costs less than branching on the wave
+        r.vr[4] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_int2*)(R + vro_t));
+        r.sc = *(const lds_float*)(R + sco);
     };
     // piece j of 0..9: K halves 0..3, V blocks 4..7, the tail block 8, the scales 9
     auto widen_store = [&](int n, const WidenRegs& r, int j) __attribute__((always_inline)) {
@@ -1130,18 +1136,15 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
             *(lds_half8*)(H + kFaHK + (w + 4 * (j - 4)) * 1024 + 16 * l) =
                 widen_i8x8((unsigned)r.vr[j - 4].x, (unsigned)r.vr[j - 4].y);
         } else if (j == 8) {
-            if (w == 0) {
-                // rows 12..15 of the tail block are the v_scale bytes: widened from 0 they are
-                // exactly 1152, so O^T rows 252..255 of that block accumulate 1152 * sum of P'
-                const int2_t vt = li >= 12 ? int2_t{0, 0} : r.vr[4];
-                *(lds_half8*)(H + kFaHK + 16 * 1024 + 16 * l) = widen_i8x8((unsigned)vt.x, (unsigned)vt.y);
-            }
+            // rows 12..15 of the tail block are the v_scale bytes: widened from 0 they are
+            // exactly 1152, so O^T rows 252..255 of that block accumulate 1152 * sum of P'
+            const int2_t vt = li >= 12 ? int2_t{0, 0} : r.vr[4];
+            *(lds_half8*)(H + kFaHK + 16 * 1024 + 16 * l) = widen_i8x8((unsigned)vt.x, (unsigned)vt.y);
         } else {
-            if (w == 1 && l < 32) {
-                // keys past seq_len may hold garbage scales (even NaN): v_scale 0 makes P' 0
-                *(lds_float*)(H + kFaHK + kFaHV + 4 * l) = r.ks;
-                *(lds_float*)(H + kFaHK + kFaHV + 128 + 4 * l) = n * kTile + l < hi ? r.vs : 0.f;
-            }
+            // k_scale * scale * log2(e) [32] then v_scale [32]; keys past seq_len may hold garbage
+            // scales (even NaN): v_scale 0 makes their P' 0
+            const bool dead = l >= 32 && n * kTile + sr >= hi;
+            *(lds_float*)(H + kFaHK + kFaHV + 4 * l) = dead ? 0.f : r.sc * sc_mul;
         }
     };
     auto widen = [&](int n) __attribute__((always_inline)) {
@@ -1151,9 +1154,6 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
         for (int j = 0; j < 10; ++j) widen_store(n, r, j);
     };
 
-    // Relative scores carry +kPLog2: p' = 2^(s - m + kPLog2) = 16 p, so P' = p' * v_scale spans the
-    // same fp16 range as in the decode kernel; l accumulates p' and the final 1 / l removes it.
-    constexpr float kPLog2 = 4.0f;
 
     // ---- front half of tile n: S^T = K Q^T from fp16 buffer n & 1 (widening tile n + 1 in
     //      between), relative scores; true when some row's running max must be raised.
@@ -1192,11 +1192,10 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
             __builtin_amdgcn_sched_barrier(0);
         }
         const int kb = n * kTile;
-        bool need = false;
+        uint64_t need = 0;
 #pragma unroll
         for (int rb = 0; rb < kFaRB; ++rb) {
-            const bool fresh = m_run[rb] == kNegInf;
-            const float nm = (fresh ? 0.f : -m_run[rb]) + kPLog2;
+            const float nm = nm_run[rb];
             float mx = kNegInf;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -1210,9 +1209,9 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
                 }
                 mx = fmaxf(mx, sv[rb][e]);
             }
-            need |= fresh ? mx > kNegInf : mx > kLazy + kPLog2;
+            need |= __builtin_amdgcn_ballot_w64(mx > thr_run[rb]);
         }
-        return need;
+        return need != 0;
     };
 
     // ---- rare path: raise the running max of the rows that need it, shift their scores, rescale
@@ -1233,6 +1232,8 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
             const float shift = raise ? mrow : 0.f;
             const float alpha = fresh ? 0.f : __builtin_amdgcn_exp2f(-shift);
             if (raise) m_run[rb] = fresh ? mrow : m_run[rb] + mrow;
+            nm_run[rb] = m_run[rb] == kNegInf ? kPLog2 : kPLog2 - m_run[rb];
+            thr_run[rb] = m_run[rb] == kNegInf ? kNegInf : kLazy + kPLog2;
 #pragma unroll
             for (int e = 0; e < 8; ++e) sv[rb][e] -= shift;
             l_run[rb] *= alpha;
@@ -1254,9 +1255,10 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
     //      widened in pieces between the products ----
     auto tile_back = [&](int n, const float (&sv)[kFaRB][8], const float (&vs)[8]) __attribute__((always_inline)) {
         const lds_u8* H = hbuf(n) + kFaHK + 16 * l;
-        const bool wnext = n + 1 < ntiles;
+        // tile n + 1 is widened even past the last tile: raw slots of tiles never copied hold stale
+        // bytes, and the fp16 buffer they land in is never read
         WidenRegs wr;
-        if (wnext) widen_load(n + 1, wr);
+        widen_load(n + 1, wr);
         constexpr int kVAhead = 4;  // V operand reads in flight ahead of their MFMAs
         half8_t vf[17];
 #pragma unroll
@@ -1280,7 +1282,7 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
 #pragma unroll
             for (int rb = 0; rb < kFaRB; ++rb)
                 oacc[rb][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[m], pop[rb], oacc[rb][m], 0, 0, 0);
-            if (m >= 2 && m < 12 && wnext) widen_store(n + 1, wr, m - 2);
+            if (m >= 2 && m < 12) widen_store(n + 1, wr, m - 2);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -1305,6 +1307,21 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
             }
             const unsigned slot = lds_base + kLdsRaw + (unsigned)((n & (kFaRaw - 1)) * kSlot);
             wait_lds();
+            if constexpr (kFast) {
+                // this wave's quarter: K blocks and V blocks 2 w, 2 w + 1 (rows of 16-key block w / 2),
+                // and the tail for wave 3
+                const int8_t* base = (w >> 1) ? src.base[1] : src.base[0];
+                const int q2 = 2 * (w & 1);
+                dma16_s(base + (int64_t)(4 * q2) * a.k_ss, dl.kvo, slot + kImgK + (2 * w) * kBlk);
+                dma16_s(base + (int64_t)(4 * q2 + 4) * a.k_ss, dl.kvo, slot + kImgK + (2 * w + 1) * kBlk);
+                dma16_s(base + (int64_t)q2 * a.k_ss, dl.vvo, slot + kImgV + (2 * w) * kBlk);
+                dma16_s(base + (int64_t)(q2 + 1) * a.k_ss, dl.vvo, slot + kImgV + (2 * w + 1) * kBlk);
+                if (w == 3) {
+                    const int64_t delta = src.base[1] - src.base[0];
+                    dma16_v<0>(src.base[0] + (delta & -(int64_t)dl.tsel) + dl.toff, slot + kImgT);
+                }
+                return;
+            }
             switch (w) {
                 case 0: issue_quarter<kFast, 0>(a, src, dl, slot, l); break;
                 case 1: issue_quarter<kFast, 1>(a, src, dl, slot, l); break;
