@@ -14,6 +14,11 @@ stream the kernels run on. The split-K partial kernel, which moves the KV bytes,
 same way on its own for the roofline. The CPU baseline is the float64 oracle on this host.
 
 Prints one JSON line.
+
+`--prefill` instead measures the chunked-prefill operator (forward_pth interface) on a 2048-token
+causal chunk over 61,440 cached tokens (63,488 keys), 24 q / 4 kv heads, block_size 16: one step
+is one operator call; the line reports TFLOP/s against the fp16 MFMA peak, and the CPU baseline is
+the float64 oracle on a sample of query rows.
 """
 import argparse
 import json
@@ -30,6 +35,8 @@ sys.path.insert(0, ROOT)
 
 METRIC = "µs/layer + achieved KV GB/s (% of HBM peak), MTP 24-row decode at 61k ctx"
 HBM_PEAK_GBS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+PREFILL_METRIC = "TFLOP/s (MFMA fp16 peak 2.5 PF/s), 2048-token int8-KV chunked prefill over 63,488 keys"
 NSEG = 128
 CALIB_BYTES = 256 << 20
 CALIB_COPIES = 8
@@ -146,6 +153,9 @@ def main():
                     help="no GPU work: turn two rocprofv3 --pmc runs of --profile-only (FETCH_SIZE, WRITE_SIZE) "
                          "into HBM bytes per partial launch, written to --traffic-out")
     ap.add_argument("--traffic-out", default=os.path.join(ROOT, "profiles", "pd_partial_mtp61k_traffic.json"))
+    ap.add_argument("--prefill", action="store_true", help="measure the chunked-prefill operator instead")
+    ap.add_argument("--chunk", type=int, default=2048, help="--prefill: query tokens per chunk")
+    ap.add_argument("--cpu-rows", type=int, default=24, help="--prefill: query rows in the CPU baseline sample")
     args = ap.parse_args()
 
     if args.traffic_summary:
@@ -167,6 +177,10 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+
+    if args.prefill:
+        bench_prefill(args, torch, kvc, pd, dev)
+        return
 
     seed = 1002
     case = build_workload(kvc, args.ctx, args.qlen, seed)
@@ -312,6 +326,93 @@ def main():
                      "bytes_per_launch": partial_bytes},
         "hot_cache_us_per_layer": None if ms_hot is None else round(ms_hot * 1e3, 3),
         "tflops": round(flops / (ms_rot * 1e-3) / 1e12, 2),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+def bench_prefill(args, torch, kvc, pd, dev):
+    """One JSON line for the chunked-prefill operator (see the module docstring)."""
+    ctx, sq = args.ctx, args.chunk
+    steps = max(1, min(args.steps, 200)) if args.steps != 4000 else 20
+    warm = max(1, min(args.warmup, 20)) if args.warmup != 200 else 3
+    case = kvc.make_case([ctx], [sq], num_q_heads=24, num_kv_heads=4, block_size=16, seed=1005)
+    flops = kvc.prefill_flops([ctx + sq], [ctx], sq, 24)
+    d = case.to(dev)
+    caches = [d.cache, kvc.clone_cache(d.cache)]
+    q = kvc.prefill_query(d)
+    qa = torch.tensor([ctx], dtype=torch.int32, device=dev)
+    out = torch.empty((1, sq, 24, 256), dtype=torch.float32, device=dev)
+
+    def op(c):
+        pd.forward_pth(q, c.key_cache, c.value_cache, d.block_table, d.seq_lens, d.scale, qa, out=out)
+
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for c in caches:
+            op(c)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for c in caches:
+            op(c)
+    torch.cuda.synchronize()
+    R = len(caches)
+    reps = max(1, math.ceil(steps / R))
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, math.ceil(warm / R))):
+            g.replay()
+        ms = time_graph(torch, g, reps, stream) / R
+    tflops = flops / (ms * 1e-3) / 1e12
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        import numpy as np
+
+        from oracle import attention as orc
+
+        rows = np.linspace(0, sq - 1, args.cpu_rows).astype(int).tolist()
+        qcpu = kvc.prefill_query(case)
+        qa_cpu = torch.tensor([ctx], dtype=torch.int32)
+
+        def cpu_once():
+            orc.paged_prefill(qcpu, case.cache.key_cache, case.cache.value_cache, case.cache.k_scale,
+                              case.cache.v_scale, case.block_table, case.seq_lens, case.scale, qa_cpu, rows)
+
+        cpu_once()
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            cpu_once()
+            times.append(time.perf_counter() - t0)
+        med = float(np.median(times))
+        sample_flops = 4 * 256 * 24 * sum(min(ctx + sq, ctx + r + 1) for r in rows)
+        cpu = {"value": round(sample_flops / med / 1e12, 6), "unit": "TFLOP/s", "cores": os.cpu_count(),
+               "kind": "port",
+               "sample": f"float64 numpy oracle (oracle/attention.py paged_prefill) on {len(rows)} of the {sq} "
+                         f"query rows (all 24 heads, full visible context each), median of 3 runs after 1 "
+                         f"warm-up, BLAS threads on {os.cpu_count()} cores ({cpu_model()})",
+               "est_ms_full_chunk": round(flops / (sample_flops / med) * 1e3, 1)}
+
+    line = {
+        "metric": PREFILL_METRIC,
+        "value": round(tflops, 1),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": reps * R,
+        "warmup": max(1, math.ceil(warm / R)) * R,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 KV widened to fp16 / fp16 MFMA / fp32 accumulate",
+        "data": "synthetic (seeded N(0,1) K/V quantised absmax/127, fp16-valued Q, random page permutation)",
+        "config": {"workload": f"chunked prefill: 1 seq, {sq}-token causal chunk over {ctx} cached tokens "
+                               f"({ctx + sq} keys), 24 q / 4 kv heads, head_dim 256, int8 per-token-head "
+                               f"paged KV, block_size 16", "flops": flops, "rotating_caches": R},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_FP16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "pd_prefill_kernel", "avg_launch_us": round(ms * 1e3, 2)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

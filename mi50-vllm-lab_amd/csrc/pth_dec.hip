@@ -784,17 +784,8 @@ __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = tid & 15, sg = tid >> 4;
 
-    // sequence of this token = number of sequences whose query rows end at or before it
-    int b = 0;
-    for (int i0 = 0; i0 < a.num_seqs; i0 += 64) {
-        const int i = i0 + lane + 1;
-        const bool ended = i <= a.num_seqs && a.qsl[i] <= tok;
-        b += __popcll(__ballot(ended));
-    }
-    if (b >= a.num_seqs || tok < a.qsl[b]) return;  // padding token
-    if (a.seq_lens[b] <= 0) return;
-    if (tok - a.qsl[b] >= a.qmax) return;  // rows past qmax are not computed
-
+    // The partial loads go out first: they are in bounds for every (token, head) of the grid, and
+    // the sequence lookup below (two dependent small loads) then overlaps their latency.
     const int64_t base = ((int64_t)tok * Hq + head) * a.nseg;
     const float* pm = a.part_m + base;
     const float* pl = a.part_l + base;
@@ -810,6 +801,17 @@ __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) 
         lv[i] = ok ? pl[sgi] : 0.f;
         ov[i] = ok ? po[(int64_t)sgi * (kDim / 4)] : (float4_t)0.f;
     }
+
+    // sequence of this token = number of sequences whose query rows end at or before it
+    int b = 0;
+    for (int i0 = 0; i0 < a.num_seqs; i0 += 64) {
+        const int i = i0 + lane + 1;
+        const bool ended = i <= a.num_seqs && a.qsl[i] <= tok;
+        b += __popcll(__ballot(ended));
+    }
+    if (b >= a.num_seqs || tok < a.qsl[b]) return;  // padding token
+    if (a.seq_lens[b] <= 0) return;
+    if (tok - a.qsl[b] >= a.qmax) return;  // rows past qmax are not computed
     float mx = kNegInf;
 #pragma unroll
     for (int i = 0; i < kCombPer; ++i) mx = fmaxf(mx, mv[i]);
