@@ -20,6 +20,7 @@
  *   pth_dec_decode             <- decode, kernels/pth_dec/pth_dec.cpp:43-91 (the torch op body,
  *                                 with tensors passed as pd_tensor descriptors)
  *   pth_fa_forward             <- forward_pth, kernels/fa_pth/pth_fa.cpp:41-85 (chunked prefill)
+ *   pth_cache_write            <- vLLM's int8 per-token-head cache update (do_kv_cache_update)
  */
 #ifndef PTH_DEC_H
 #define PTH_DEC_H
@@ -36,6 +37,8 @@ extern "C" {
 #define PD_DTYPE_FP16 2
 #define PD_DTYPE_FP32 3
 #define PD_DTYPE_INT32 4
+#define PD_DTYPE_BF16 5
+#define PD_DTYPE_INT64 6
 
 #define PD_MAX_DIMS 4
 
@@ -134,6 +137,24 @@ int pth_fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_tens
                    const pd_tensor* block_table, const pd_tensor* seq_lens, double scale,
                    const pd_tensor* q_abs_offset, const pd_tensor* out, hipStream_t stream, char* err,
                    int errlen);
+
+/*
+ * KV-cache writer and quantiser: the producer of the 520-byte rows the two operators read.
+ * Replaces vLLM's cache update for int8 per-token-head KV, which the reference calls as
+ * do_kv_cache_update(layer, key, value, kv_cache, slot_mapping)
+ * (upstream/pr-dflash2/0002-fix-gfx906-keep-the-drafter-s-sliding-window-in-the-.patch:81-87;
+ * the update itself lives in the un-vendored vLLM fork KIntegrated/vllm-gfx906-mobydick 0.30.0).
+ *   key, value   fp16, bf16 or fp32 [T, Hkv, 256], unit dim stride
+ *   key_cache, value_cache, k_scale, v_scale   the cache views (as for pth_dec_decode)
+ *   slot_mapping int64 [T]: slot = block * block_size + offset; negative slots (padding) and
+ *                slots past the cache are skipped
+ * Per (token, kv head): scale = absmax / 127 (0 for an all-zero row), q = clamp(rint(x / scale),
+ * -127, 127) with x / scale correctly rounded. Returns 0, 1 (validation failure, message in
+ * err) or 2 (launch failure).
+ */
+int pth_cache_write(const pd_tensor* key, const pd_tensor* value, const pd_tensor* key_cache,
+                    const pd_tensor* value_cache, const pd_tensor* k_scale, const pd_tensor* v_scale,
+                    const pd_tensor* slot_mapping, hipStream_t stream, char* err, int errlen);
 
 #ifdef __cplusplus
 }

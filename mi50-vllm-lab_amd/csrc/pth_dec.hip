@@ -1386,6 +1386,72 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
 }
 
 // ---------------------------------------------------------------------------------------
+// KV-cache writer: the producer of the 520-byte rows (vLLM's cache update for int8
+// per-token-head KV, called as do_kv_cache_update(layer, key, value, kv_cache, slot_mapping),
+// upstream/pr-dflash2/0002-fix-gfx906-keep-the-drafter-s-sliding-window-in-the-.patch:81-87).
+// One wave per (token, kv head): 64 lanes x 4 elements of K and of V; absmax by a wave
+// reduction, scale = absmax / 127 (0 for an all-zero row), q = clamp(rint(x / scale), -127, 127)
+// with x / scale correctly rounded; the row's K bytes, k_scale, V bytes and v_scale are written
+// with 4-byte stores. Tokens whose slot is negative (padding) or past the cache are skipped.
+struct CacheWriteParams {
+    const void* key;
+    const void* value;
+    int64_t k_st, k_sh, v_st, v_sh;  // elements between tokens / heads of key and value
+    int8_t* kc;
+    int64_t k_sb, k_ss, k_sh_c;      // cache bytes between blocks / slots / kv heads
+    const int64_t* slots;
+    int64_t num_slots;               // blocks * block_size
+    int T, Hkv, block_size;
+};
+
+template <class In>
+__device__ __forceinline__ float4_t load4(const In* p) {
+    if constexpr (sizeof(In) == 4) {
+        return *reinterpret_cast<const float4_t*>(p);
+    } else {
+        typedef In in4_t __attribute__((ext_vector_type(4)));
+        const in4_t v = *reinterpret_cast<const in4_t*>(p);
+        return float4_t{(float)v.x, (float)v.y, (float)v.z, (float)v.w};
+    }
+}
+
+__device__ __forceinline__ unsigned quant4(float4_t x, float scale) {
+    if (scale == 0.f) return 0u;
+    auto q = [&](float v) -> unsigned {
+        const float r = fminf(fmaxf(__builtin_rintf(v / scale), -127.f), 127.f);
+        return (unsigned)((int)r & 0xff);
+    };
+    return q(x.x) | (q(x.y) << 8) | (q(x.z) << 16) | (q(x.w) << 24);
+}
+
+template <class In>
+__global__ void __launch_bounds__(256) pd_cache_write_kernel(const CacheWriteParams a) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+    if (row >= a.T * a.Hkv) return;
+    const int t = row / a.Hkv, h = row - t * a.Hkv;
+    const int64_t slot = a.slots[t];
+    if (slot < 0 || slot >= a.num_slots) return;
+    const float4_t k = load4(static_cast<const In*>(a.key) + t * a.k_st + h * a.k_sh + 4 * l);
+    const float4_t v = load4(static_cast<const In*>(a.value) + t * a.v_st + h * a.v_sh + 4 * l);
+    float km = fmaxf(fmaxf(fabsf(k.x), fabsf(k.y)), fmaxf(fabsf(k.z), fabsf(k.w)));
+    float vm = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        km = fmaxf(km, __shfl_xor(km, o, 64));
+        vm = fmaxf(vm, __shfl_xor(vm, o, 64));
+    }
+    const float ks = km / 127.f, vs = vm / 127.f;
+    const int64_t blk = slot / a.block_size, off = slot - blk * a.block_size;
+    int8_t* r = a.kc + blk * a.k_sb + off * a.k_ss + h * a.k_sh_c;
+    reinterpret_cast<unsigned*>(r)[l] = quant4(k, ks);
+    reinterpret_cast<unsigned*>(r + 260)[l] = quant4(v, vs);
+    if (l == 0) {
+        *reinterpret_cast<float*>(r + 256) = ks;
+        *reinterpret_cast<float*>(r + 516) = vs;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
 // host side
 
 struct LaunchArgs {
@@ -1783,6 +1849,64 @@ int pth_fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_tens
     if (e != hipSuccess) {
         char msg[256];
         snprintf(msg, sizeof msg, "pth_fa launch failed: %s", hipGetErrorString(e));
+        fail(err, errlen, msg);
+        return 2;
+    }
+    return 0;
+}
+
+int pth_cache_write(const pd_tensor* key, const pd_tensor* value, const pd_tensor* key_cache,
+                    const pd_tensor* value_cache, const pd_tensor* k_scale, const pd_tensor* v_scale,
+                    const pd_tensor* slot_mapping, hipStream_t stream, char* err, int errlen) {
+    if (!key || !value || !key_cache || !value_cache || !k_scale || !v_scale || !slot_mapping)
+        return fail(err, errlen, "null tensor descriptor");
+    if (!layout_ok(key_cache, value_cache, k_scale, v_scale))
+        return fail(err, errlen, "KV cache views do not have the int8 per-token-head row layout");
+    const int dt = key->dtype;
+    if (!((dt == PD_DTYPE_FP16 || dt == PD_DTYPE_BF16 || dt == PD_DTYPE_FP32) && value->dtype == dt))
+        return fail(err, errlen, "key and value must be fp16, bf16 or fp32 of the same dtype");
+    const int64_t T = key->sizes[0], Hkv = key_cache->sizes[2];
+    if (!(key->ndim == 3 && value->ndim == 3 && key->sizes[1] == Hkv && value->sizes[1] == Hkv &&
+          key->sizes[2] == 256 && value->sizes[2] == 256 && value->sizes[0] == T && key->strides[2] == 1 &&
+          value->strides[2] == 1))
+        return fail(err, errlen, "key and value must be [T, Hkv, 256] with unit dim stride");
+    const int64_t esz = dt == PD_DTYPE_FP32 ? 4 : 2;
+    const int64_t vec = 4 * esz;  // each lane loads 4 elements
+    if (!((reinterpret_cast<uintptr_t>(key->data) % vec) == 0 && (reinterpret_cast<uintptr_t>(value->data) % vec) == 0 &&
+          key->strides[0] % 4 == 0 && key->strides[1] % 4 == 0 && value->strides[0] % 4 == 0 &&
+          value->strides[1] % 4 == 0))
+        return fail(err, errlen, "key and value rows must be aligned to 4 elements");
+    if (!(slot_mapping->dtype == PD_DTYPE_INT64 && slot_mapping->ndim == 1 && slot_mapping->sizes[0] >= T &&
+          (slot_mapping->strides[0] == 1 || slot_mapping->sizes[0] <= 1)))
+        return fail(err, errlen, "slot_mapping must be a contiguous int64 [T]");
+    if (T == 0) return 0;
+    CacheWriteParams p;
+    p.key = key->data;
+    p.value = value->data;
+    p.k_st = key->strides[0];
+    p.k_sh = key->strides[1];
+    p.v_st = value->strides[0];
+    p.v_sh = value->strides[1];
+    p.kc = static_cast<int8_t*>(const_cast<void*>(key_cache->data));
+    p.k_sb = key_cache->strides[0];
+    p.k_ss = key_cache->strides[1];
+    p.k_sh_c = key_cache->strides[2];
+    p.slots = static_cast<const int64_t*>(slot_mapping->data);
+    p.block_size = (int)key_cache->sizes[1];
+    p.num_slots = key_cache->sizes[0] * key_cache->sizes[1];
+    p.T = (int)T;
+    p.Hkv = (int)Hkv;
+    const dim3 grid((unsigned)((T * Hkv + 3) / 4));
+    if (dt == PD_DTYPE_FP16)
+        hipLaunchKernelGGL((pd_cache_write_kernel<_Float16>), grid, dim3(256), 0, stream, p);
+    else if (dt == PD_DTYPE_BF16)
+        hipLaunchKernelGGL((pd_cache_write_kernel<__bf16>), grid, dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL((pd_cache_write_kernel<float>), grid, dim3(256), 0, stream, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        char msg[256];
+        snprintf(msg, sizeof msg, "cache write launch failed: %s", hipGetErrorString(e));
         fail(err, errlen, msg);
         return 2;
     }

@@ -25,6 +25,8 @@ PD_DTYPE_INT8 = 1
 PD_DTYPE_FP16 = 2
 PD_DTYPE_FP32 = 3
 PD_DTYPE_INT32 = 4
+PD_DTYPE_BF16 = 5
+PD_DTYPE_INT64 = 6
 PD_MAX_DIMS = 4
 
 _DTYPES = {
@@ -32,6 +34,8 @@ _DTYPES = {
     torch.float16: PD_DTYPE_FP16,
     torch.float32: PD_DTYPE_FP32,
     torch.int32: PD_DTYPE_INT32,
+    torch.bfloat16: PD_DTYPE_BF16,
+    torch.int64: PD_DTYPE_INT64,
 }
 
 # Every symbol include/pth_dec.h declares.
@@ -44,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "pth_dec_decode",
     "pth_dec_version",
     "pth_fa_forward",
+    "pth_cache_write",
 )
 
 
@@ -93,6 +98,8 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.pth_dec_decode.restype = c_int
     lib.pth_fa_forward.argtypes = [tp] * 5 + [c_double, tp, tp, vp, ctypes.c_char_p, c_int]
     lib.pth_fa_forward.restype = c_int
+    lib.pth_cache_write.argtypes = [tp] * 7 + [vp, ctypes.c_char_p, c_int]
+    lib.pth_cache_write.restype = c_int
     lib.pth_dec_version.argtypes = []
     lib.pth_dec_version.restype = ctypes.c_char_p
     if path is None:
@@ -177,6 +184,26 @@ def forward_pth(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Ten
     if rc != 0:
         raise RuntimeError(err.value.decode())
     return out
+
+
+def cache_write(key: torch.Tensor, value: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                k_scale: torch.Tensor, v_scale: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """Quantise key/value [T, Hkv, 256] per (token, kv head) into the int8 rows at slot_mapping.
+
+    scale = absmax / 127, q = clamp(rint(x / scale), -127, 127); negative slots are skipped.
+    Replaces vLLM's int8 per-token-head cache update (do_kv_cache_update,
+    upstream/pr-dflash2/0002-fix-gfx906-keep-the-drafter-s-sliding-window-in-the-.patch:81-87).
+    """
+    if not key.is_cuda:
+        raise RuntimeError("key and value must be fp16, bf16 or fp32 of the same dtype")
+    lib = load_library()
+    descs = [describe(t) for t in (key, value, key_cache, value_cache, k_scale, v_scale, slot_mapping)]
+    err = ctypes.create_string_buffer(256)
+    with torch.cuda.device(key.device):
+        stream = torch.cuda.current_stream(key.device).cuda_stream
+        rc = lib.pth_cache_write(*[ctypes.byref(x) for x in descs], ctypes.c_void_p(stream), err, len(err))
+    if rc != 0:
+        raise RuntimeError(err.value.decode())
 
 
 def _ptr(t: torch.Tensor, ctype):

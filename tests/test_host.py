@@ -29,7 +29,7 @@ def lib():
 def declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(pth_(?:dec|fa)_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(pth_(?:dec|fa|cache)_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_header_symbols_exported(lib):
@@ -222,3 +222,31 @@ def test_python_prefill_refuses_host_tensors():
     with pytest.raises(RuntimeError):
         pth_dec.forward_pth(kvc.prefill_query(case), c.key_cache, c.value_cache, case.block_table, case.seq_lens,
                             case.scale, torch.tensor(case.ctxs, dtype=torch.int32))
+
+
+def test_cache_write_validation_messages(lib):
+    case = make()
+    c = case.cache
+    k = torch.zeros((3, 2, 256), dtype=torch.float16)
+    slots = torch.zeros(3, dtype=torch.int64)
+
+    def call(key=k, value=k, kc=c.key_cache, slot_mapping=slots):
+        descs = [pth_dec.describe(t) for t in (key, value, kc, c.value_cache, c.k_scale, c.v_scale, slot_mapping)]
+        err = ctypes.create_string_buffer(256)
+        rc = lib.pth_cache_write(*[ctypes.byref(x) for x in descs], None, err, len(err))
+        return rc, err.value.decode()
+
+    cases = [
+        (dict(kc=c.value_cache), "KV cache views"),
+        (dict(key=k.to(torch.int32)), "fp16, bf16 or fp32"),
+        (dict(value=k.float()), "fp16, bf16 or fp32"),
+        (dict(key=torch.zeros((3, 3, 256), dtype=torch.float16)), "[T, Hkv, 256]"),
+        (dict(key=torch.zeros((3, 2, 512), dtype=torch.float16)[..., ::2]), "[T, Hkv, 256]"),
+        (dict(slot_mapping=slots.int()), "int64 [T]"),
+        (dict(slot_mapping=slots[:2]), "int64 [T]"),
+    ]
+    for kw, msg in cases:
+        rc, text = call(**kw)
+        assert rc == 1 and msg in text, (list(kw), rc, text)
+    rc, text = call(key=k[:0], value=k[:0], slot_mapping=slots[:0])
+    assert rc == 0, text
