@@ -1,0 +1,205 @@
+"""Routing shim between vLLM's Triton attention backend and the gfx950 int8-KV operators.
+
+Restates the reference's backend patch (patches/vllm/triton_attn.patch) for this library, in a
+form that does not import vLLM (absent here): the backend keeps its own objects and passes the
+few fields the routing reads.
+
+- Loaders (triton_attn.patch:15-70): the library is loaded once per process and cached; an
+  environment switch turns each path off, and a load failure logs a warning and leaves the
+  backend on Triton. Both operators live in one library (libpthdec.so).
+- Gating (triton_attn.patch:91-114): int8 per-token-head KV, ROCm, decoder attention, head
+  size 256, no sinks / alibi / softcap / chunked lookback / TD, on gfx950. Prefill also needs no
+  sliding window. Decode accepts a left sliding window (the operator implements the window
+  rule) and any GQA group with qmax * G <= 48, where the reference required GQA 6 and no window.
+- forward_pth_dec (triton_attn.patch:116-174): the cache layout is checked once; the call falls
+  back (returns False) without the softmax segment buffers, with more query tokens than segment
+  rows, or with query / output strides the operator does not take. nsplit = min(splits,
+  segment count).
+- forward_pth_fa (triton_attn.patch:176-262): the sequences with >= MIN_Q query tokens must form
+  a suffix of the batch; the rows before it go to the decode operator when every prefix sequence
+  has <= 4 (8 with DFlash) query tokens, else to the caller's Triton function. Each suffix
+  sequence runs the prefill operator once (no padding to a tile ladder is needed).
+- route (triton_attn.patch:272-308): prefill first when max_seqlen_q >= MIN_Q, then decode
+  when max_seqlen_q <= MAX_Q; causal only, no multimodal prefix, no RSWA prefix, no output
+  scale. Returns False when the caller must run its own path.
+"""
+from __future__ import annotations
+
+import logging
+import os
+from dataclasses import dataclass
+from typing import Any, Callable, Optional
+
+import torch
+
+from . import pth_dec as _pd
+
+logger = logging.getLogger(__name__)
+
+PTH_FA_MIN_Q = int(os.environ.get("VLLM_GFX950_PTH_FA_MIN_Q", "64"))
+PTH_DEC_MAX_Q = int(os.environ.get("VLLM_GFX950_PTH_DEC_MAX_Q", "4"))
+PTH_DEC_SPLITS = int(os.environ.get("VLLM_GFX950_PTH_DEC_SPLITS", "64"))
+MAX_ROWS_PER_KV_HEAD = 48  # qmax * G the decode operator takes
+
+_dec_mod = None
+_fa_mod = None
+
+
+class _Operators:
+    """The operator entry points the shim calls (the reference's torch-extension modules)."""
+
+    def __init__(self, path: Optional[str]):
+        _pd.load_library(path)
+        self.supported_layout = _pd.supported_layout
+        self.decode = _pd.decode
+        self.forward_pth = _pd.forward_pth
+
+
+def _load(env_switch: str, env_lib: str, what: str):
+    path = os.environ.get(env_lib) or None
+    if os.environ.get(env_switch, "1") != "1":
+        return None
+    if path is not None and not os.path.exists(path):
+        logger.warning("gfx950: %s not found; %s stays on Triton", path, what)
+        return None
+    try:
+        return _Operators(path)
+    except Exception as e:  # keep serving on the Triton path
+        logger.warning("gfx950: could not load %s (%s); %s stays on Triton", path or _pd.LIB_PATH, e, what)
+        return None
+
+
+def load_pth_dec():
+    """The decode operator, or None (VLLM_GFX950_PTH_DEC=0 or load failure). Cached."""
+    global _dec_mod
+    if _dec_mod is None:
+        _dec_mod = _load("VLLM_GFX950_PTH_DEC", "VLLM_GFX950_PTH_DEC_LIB", "decode") or False
+    return _dec_mod or None
+
+
+def load_pth_fa():
+    """The prefill operator, or None (VLLM_GFX950_PTH_FA=0 or load failure). Cached."""
+    global _fa_mod
+    if _fa_mod is None:
+        _fa_mod = _load("VLLM_GFX950_PTH_FA", "VLLM_GFX950_PTH_FA_LIB", "prefill") or False
+    return _fa_mod or None
+
+
+def reset_loaders() -> None:
+    """Forget the cached loaders (tests)."""
+    global _dec_mod, _fa_mod
+    _dec_mod = None
+    _fa_mod = None
+
+
+@dataclass
+class AttnMeta:
+    """The fields of vLLM's TritonAttentionMetadata the routing reads."""
+    query_start_loc: torch.Tensor            # int32 [B + 1], device
+    query_start_loc_cpu: Any                 # the same offsets on the host (list or tensor)
+    seq_lens: torch.Tensor                   # int32 [B], device
+    block_table: torch.Tensor                # int32 [B, max_blocks], device
+    max_seq_len: int = 0
+    causal: bool = True
+    softmax_segm_output: Optional[torch.Tensor] = None   # fp32 [T, Hq, nseg, 256]
+    softmax_segm_max: Optional[torch.Tensor] = None      # fp32 [T, Hq, nseg]
+    softmax_segm_expsum: Optional[torch.Tensor] = None   # fp32 [T, Hq, nseg]
+    mm_prefix_range_tensor: Optional[torch.Tensor] = None
+    rswa_prefix_lens: Optional[torch.Tensor] = None
+
+
+class Gfx950Int8Attention:
+    """Per-layer routing state (the part of TritonAttentionImpl the patch adds)."""
+
+    def __init__(self, *, num_heads: int, num_kv_heads: int, head_size: int, scale: float,
+                 kv_quant_int8_per_token_head: bool, is_rocm: bool, is_decoder: bool,
+                 sliding_window=(-1, -1), sinks=None, alibi_slopes=None, logits_soft_cap=0.0,
+                 chunk_lookback: int = -1, use_td: bool = False, on_gfx950: bool = True,
+                 max_q: int = PTH_DEC_MAX_Q):
+        self.scale = float(scale)
+        self.num_heads, self.num_kv_heads = num_heads, num_kv_heads
+        self.pth_fa = None
+        self.pth_dec = None
+        self.layout_ok: Optional[bool] = None  # cache layout, checked on first use
+        self.max_q = max_q
+        # left window W: vLLM's sliding_window (W - 1, 0); -1 = none
+        self.window = sliding_window[0] + 1 if sliding_window[0] >= 0 else -1
+        common = (kv_quant_int8_per_token_head and is_rocm and is_decoder and head_size == 256 and sinks is None
+                  and alibi_slopes is None and not logits_soft_cap and chunk_lookback == -1 and not use_td
+                  and on_gfx950)
+        if not common:
+            return
+        if self.window < 0 and sliding_window[1] < 0:
+            self.pth_fa = load_pth_fa()
+        G = num_heads // num_kv_heads if num_kv_heads > 0 else 0
+        if num_heads % max(num_kv_heads, 1) == 0 and 1 <= max_q * G <= MAX_ROWS_PER_KV_HEAD and sliding_window[1] < 0:
+            self.pth_dec = load_pth_dec()
+
+    # -------------------------------------------------------------------------------------
+    def forward_pth_dec(self, query, key_cache, value_cache, k_scale_cache, v_scale_cache, block_table, seq_lens,
+                        query_start_loc, output, max_q: int, meta: AttnMeta) -> bool:
+        """Sequences with <= max_q query tokens through the decode operator. Launch only (no host
+        sync, no allocation): safe in graphs. False: the caller runs its own path."""
+        if self.layout_ok is None:
+            self.layout_ok = bool(self.pth_dec.supported_layout(key_cache, value_cache, k_scale_cache,
+                                                                v_scale_cache))
+            if not self.layout_ok:
+                logger.warning("gfx950: unexpected int8 KV cache layout; decode stays on Triton")
+        segm_o = meta.softmax_segm_output
+        if (not self.layout_ok or segm_o is None or meta.softmax_segm_max is None or meta.softmax_segm_expsum is None
+                or query.shape[0] > segm_o.shape[0] or query.dim() != 3 or output.dim() != 3
+                or query.stride(1) != query.shape[2] or query.stride(2) != 1 or output.stride(2) != 1):
+            return False
+        self.pth_dec.decode(query, key_cache, value_cache, k_scale_cache, v_scale_cache, block_table, seq_lens,
+                            query_start_loc, output, self.scale, segm_o, meta.softmax_segm_max,
+                            meta.softmax_segm_expsum, seq_lens.shape[0], max(1, max_q),
+                            min(PTH_DEC_SPLITS, segm_o.shape[2]), window=self.window, causal=True)
+        return True
+
+    # -------------------------------------------------------------------------------------
+    def forward_pth_fa(self, query, key_cache, value_cache, k_scale_cache, v_scale_cache, meta: AttnMeta, output,
+                       triton_fallback: Callable[..., None]) -> bool:
+        """The suffix of sequences with >= PTH_FA_MIN_Q query tokens through the prefill
+        operator; the rows before it through the decode operator or `triton_fallback(start, end,
+        seq_begin, seq_end, max_q)`. False when there is no such suffix."""
+        qsl = [int(x) for x in (meta.query_start_loc_cpu.tolist() if hasattr(meta.query_start_loc_cpu, "tolist")
+                                else meta.query_start_loc_cpu)]
+        n = len(qsl) - 1
+        p = n
+        while p > 0 and qsl[p] - qsl[p - 1] >= PTH_FA_MIN_Q:
+            p -= 1
+        if p == n:
+            return False
+        max_q_prefix = max((qsl[i + 1] - qsl[i] for i in range(p)), default=0)
+        if p > 0 and not (
+            self.pth_dec is not None and max_q_prefix <= self.max_q
+            and self.forward_pth_dec(query[:qsl[p]], key_cache, value_cache, k_scale_cache, v_scale_cache,
+                                     meta.block_table[:p], meta.seq_lens[:p], meta.query_start_loc[:p + 1],
+                                     output[:qsl[p]], max_q_prefix, meta)):
+            triton_fallback(0, qsl[p], 0, p, max_q_prefix)
+        for i in range(p, n):
+            start, nq = qsl[i], qsl[i + 1] - qsl[i]
+            q = query[start:start + nq].transpose(0, 1).unsqueeze(0).float().contiguous()  # [1, Hq, nq, D]
+            seq_len = meta.seq_lens[i:i + 1]
+            out = self.pth_fa.forward_pth(q, key_cache, value_cache, meta.block_table[i:i + 1], seq_len, self.scale,
+                                          seq_len - nq)
+            output[start:start + nq] = out[0].to(output.dtype)
+        return True
+
+    # -------------------------------------------------------------------------------------
+    def route(self, query, key_cache, value_cache, k_scale_cache, v_scale_cache, meta: AttnMeta, output,
+              max_seqlen_q: int, num_actual_tokens: int, triton_fallback: Callable[..., None],
+              output_scale=None) -> bool:
+        """The forward() glue: True when one of the operators handled the batch."""
+        plain = (meta.causal is True and meta.mm_prefix_range_tensor is None and meta.rswa_prefix_lens is None
+                 and output_scale is None)
+        if (self.pth_fa is not None and max_seqlen_q >= PTH_FA_MIN_Q and plain
+                and self.forward_pth_fa(query, key_cache, value_cache, k_scale_cache, v_scale_cache, meta, output,
+                                        triton_fallback)):
+            return True
+        if (self.pth_dec is not None and max_seqlen_q <= self.max_q and plain
+                and self.forward_pth_dec(query[:num_actual_tokens], key_cache, value_cache, k_scale_cache,
+                                         v_scale_cache, meta.block_table, meta.seq_lens, meta.query_start_loc,
+                                         output[:num_actual_tokens], max_seqlen_q, meta)):
+            return True
+        return False

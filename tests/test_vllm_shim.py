@@ -1,0 +1,180 @@
+"""CPU tests of the vLLM routing shim (mi50-vllm-lab_amd/vllm_shim.py) with recording stand-ins
+for the operators: the gating of triton_attn.patch:91-114 (and where it is relaxed), the
+thresholds and fallbacks of :116-174 and :272-308, the suffix detection of :192-198, the
+prefix routing of :199-242 and the per-sequence prefill calls of :243-262, and the loaders'
+switches and failure handling (:15-70).
+"""
+import logging
+
+import pytest
+import torch
+
+from mi50_vllm_lab_amd import vllm_shim as shim
+
+
+class FakeOps:
+    def __init__(self, layout_ok=True):
+        self.calls = []
+        self.layout_ok = layout_ok
+
+    def supported_layout(self, kc, vc, ks, vs):
+        self.calls.append(("layout",))
+        return self.layout_ok
+
+    def decode(self, q, kc, vc, ks, vs, bt, sl, qsl, out, scale, po, pm, pl, num_seqs, qmax, nsplit, window=-1,
+               causal=True):
+        self.calls.append(("decode", q.shape[0], num_seqs, qmax, nsplit, window, bt.shape[0]))
+        out.fill_(1.0)
+
+    def forward_pth(self, q, kc, vc, bt, sl, scale, q_abs):
+        self.calls.append(("prefill", tuple(q.shape), int(sl[0]), int(q_abs[0]), q.dtype))
+        return torch.full((1, q.shape[2], q.shape[1], q.shape[3]), 2.0)
+
+
+@pytest.fixture
+def ops(monkeypatch):
+    f = FakeOps()
+    monkeypatch.setattr(shim, "load_pth_dec", lambda: f)
+    monkeypatch.setattr(shim, "load_pth_fa", lambda: f)
+    return f
+
+
+def impl(**kw):
+    args = dict(num_heads=24, num_kv_heads=4, head_size=256, scale=0.0625, kv_quant_int8_per_token_head=True,
+                is_rocm=True, is_decoder=True)
+    args.update(kw)
+    return shim.Gfx950Int8Attention(**args)
+
+
+def meta(qlens, seqs, nseg=64, hq=24, segm=True, causal=True):
+    qsl = [0]
+    for q in qlens:
+        qsl.append(qsl[-1] + q)
+    T = qsl[-1]
+    return shim.AttnMeta(
+        query_start_loc=torch.tensor(qsl, dtype=torch.int32), query_start_loc_cpu=qsl,
+        seq_lens=torch.tensor(seqs, dtype=torch.int32), block_table=torch.zeros((len(seqs), 8), dtype=torch.int32),
+        max_seq_len=max(seqs), causal=causal,
+        softmax_segm_output=torch.empty((max(T, 1), hq, nseg, 256)) if segm else None,
+        softmax_segm_max=torch.empty((max(T, 1), hq, nseg)) if segm else None,
+        softmax_segm_expsum=torch.empty((max(T, 1), hq, nseg)) if segm else None)
+
+
+def tensors(T, hq=24):
+    q = torch.randn((T, hq, 256))
+    out = torch.zeros((T, hq, 256))
+    kc = torch.zeros((4, 16, 4, 260), dtype=torch.int8)
+    return q, out, kc
+
+
+@pytest.mark.parametrize("kw,fa,dec", [
+    ({}, True, True),
+    ({"kv_quant_int8_per_token_head": False}, False, False),
+    ({"is_rocm": False}, False, False),
+    ({"is_decoder": False}, False, False),
+    ({"head_size": 128}, False, False),
+    ({"sinks": torch.zeros(24)}, False, False),
+    ({"alibi_slopes": torch.zeros(24)}, False, False),
+    ({"logits_soft_cap": 30.0}, False, False),
+    ({"chunk_lookback": 128}, False, False),
+    ({"use_td": True}, False, False),
+    ({"on_gfx950": False}, False, False),
+    ({"sliding_window": (2047, -1)}, False, True),        # decode takes the window, prefill does not
+    ({"num_heads": 32, "num_kv_heads": 4}, True, True),   # G 8: 4 x 8 = 32 rows
+    ({"num_heads": 52, "num_kv_heads": 4}, True, False),  # G 13: 52 rows > 48
+])
+def test_gating(ops, kw, fa, dec):
+    a = impl(**kw)
+    assert (a.pth_fa is not None) == fa and (a.pth_dec is not None) == dec
+
+
+def test_window_is_passed_as_left_width(ops):
+    a = impl(sliding_window=(2047, -1))
+    assert a.window == 2048
+    q, out, kc = tensors(8)
+    m = meta([4, 4], [5000, 300])
+    assert a.route(q, kc, kc, None, None, m, out, 4, 8, lambda *x: None)
+    assert ops.calls[-1][5] == 2048
+
+
+def test_decode_rows_route_to_decode_with_nsplit_cap(ops):
+    a = impl()
+    q, out, kc = tensors(6)
+    m = meta([4, 1, 1], [100, 50, 7], nseg=32)
+    assert a.route(q, kc, kc, None, None, m, out, 4, 6, lambda *x: pytest.fail("fallback"))
+    assert ops.calls == [("layout",), ("decode", 6, 3, 4, 32, -1, 3)]
+    assert (out == 1).all()
+
+
+@pytest.mark.parametrize("why", ["no_segm", "too_many_tokens", "q_stride", "layout", "mid_q", "noncausal"])
+def test_decode_fallbacks(monkeypatch, why):
+    f = FakeOps(layout_ok=why != "layout")
+    monkeypatch.setattr(shim, "load_pth_dec", lambda: f)
+    monkeypatch.setattr(shim, "load_pth_fa", lambda: f)
+    a = impl()
+    q, out, kc = tensors(4)
+    m = meta([4], [100], segm=why != "no_segm", causal=why != "noncausal")
+    if why == "too_many_tokens":
+        m.softmax_segm_output = torch.empty((2, 24, 64, 256))
+    if why == "q_stride":
+        q = torch.randn((4, 24, 512))[..., :256]
+    maxq = 10 if why == "mid_q" else 4
+    assert not a.route(q, kc, kc, None, None, m, out, maxq, 4, lambda *x: None)
+    assert not any(c[0] == "decode" for c in f.calls)
+
+
+def test_layout_checked_once(ops):
+    a = impl()
+    q, out, kc = tensors(4)
+    m = meta([4], [100])
+    for _ in range(3):
+        a.route(q, kc, kc, None, None, m, out, 4, 4, lambda *x: None)
+    assert sum(1 for c in ops.calls if c[0] == "layout") == 1
+
+
+def test_prefill_suffix_with_decode_prefix(ops):
+    a = impl()
+    q, out, kc = tensors(2 + 100 + 70)
+    m = meta([1, 1, 100, 70], [500, 40, 1100, 70])
+    assert a.route(q, kc, kc, None, None, m, out, 100, 172, lambda *x: pytest.fail("fallback"))
+    dec = [c for c in ops.calls if c[0] == "decode"]
+    pre = [c for c in ops.calls if c[0] == "prefill"]
+    assert dec == [("decode", 2, 2, 1, 64, -1, 2)]
+    assert pre == [("prefill", (1, 24, 100, 256), 1100, 1000, torch.float32),
+                   ("prefill", (1, 24, 70, 256), 70, 0, torch.float32)]
+    assert (out[:2] == 1).all() and (out[2:] == 2).all()
+
+
+def test_prefill_prefix_too_long_for_decode_goes_to_triton(ops):
+    a = impl()
+    q, out, kc = tensors(10 + 80)
+    m = meta([10, 80], [200, 500])
+    seen = []
+    assert a.route(q, kc, kc, None, None, m, out, 80, 90, lambda *x: seen.append(x))
+    assert seen == [(0, 10, 0, 1, 10)]
+    assert not any(c[0] == "decode" for c in ops.calls)
+
+
+def test_no_prefill_suffix_falls_through(ops):
+    a = impl()
+    q, out, kc = tensors(100 + 1)
+    m = meta([100, 1], [300, 20])          # the long sequence is not a suffix
+    assert not a.route(q, kc, kc, None, None, m, out, 100, 101, lambda *x: pytest.fail("fallback"))
+    assert not ops.calls
+
+
+def test_loader_switches_and_failures(monkeypatch, caplog):
+    shim.reset_loaders()
+    monkeypatch.setenv("VLLM_GFX950_PTH_DEC", "0")
+    assert shim.load_pth_dec() is None
+    shim.reset_loaders()
+    monkeypatch.setenv("VLLM_GFX950_PTH_DEC", "1")
+    monkeypatch.setenv("VLLM_GFX950_PTH_DEC_LIB", "/nonexistent/libpthdec.so")
+    with caplog.at_level(logging.WARNING):
+        assert shim.load_pth_dec() is None
+    assert "stays on Triton" in caplog.text
+    shim.reset_loaders()
+    monkeypatch.delenv("VLLM_GFX950_PTH_DEC_LIB")
+    monkeypatch.setenv("VLLM_GFX950_PTH_FA", "0")
+    assert shim.load_pth_fa() is None
+    shim.reset_loaders()
