@@ -67,6 +67,7 @@ typedef __attribute__((address_space(3))) int lds_int;
 typedef __attribute__((address_space(3))) uint64_t lds_u64;
 typedef unsigned long long ull2_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) ull2_t lds_ull2;
+typedef __attribute__((address_space(3))) half8_t lds_half8;
 typedef const __attribute__((address_space(4))) int* const_int_ptr;  // scalar-cache loads
 
 constexpr int kDim = 256;             // head dim (the only one the cache row layout allows)
@@ -102,6 +103,9 @@ constexpr int kWaves = 4;                          // independent tile streams p
 constexpr int kThreads = 64 * kWaves;
 constexpr int kOPitch = kDim + 4;                  // floats per row of the merge buffer
 constexpr int kBtCache = 1024;                     // block-table entries of a split kept in LDS
+// With Q staged in LDS as well (one or two row blocks) the block-table slice is smaller:
+constexpr int kBtEarly = 384;                      // per-block row offsets (192 tiles per split)
+constexpr int kBtRaw = 384;                        // raw block-table entries of the split
 
 struct PartialParams {
     const _Float16* q;
@@ -246,6 +250,10 @@ __device__ __forceinline__ void dma16_v(const int8_t* vaddr, unsigned lds_dst) {
                  "i"(kImm)
                  : "memory", "m0");
 }
+// 4-byte copies: LDS[dst + 4 * lane] = *vaddr.
+__device__ __forceinline__ void dma4_v(const int* vaddr, unsigned lds_dst) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(vaddr), "s"(lds_dst) : "memory", "m0");
+}
 template <int N>
 __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -367,8 +375,14 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     constexpr int kLdsMerge = kWaves * kMergeRows * kOPitch * 4;
     constexpr int kLdsMain = kLdsWaves > kLdsMerge ? kLdsWaves : kLdsMerge;
     constexpr int kLdsStats = kLdsMain;                   // m, l: [wave][NRB][16]
+    // kEarly: Q and the block-table slice are copied into LDS like the tiles, and each wave's
+    // first two tiles are issued before anything is waited for (addressed with scalar
+    // block-table loads), so the copies start one memory round trip after the kernel does.
+    constexpr bool kEarly = kFast && NRB <= 2;
     constexpr int kLdsBt = kLdsStats + 2 * kWaves * NRB * 16 * 4;
-    constexpr int kLdsBytes = kLdsBt + kBtCache * 8;
+    constexpr int kLdsRaw = kLdsBt + (kEarly ? kBtEarly : kBtCache) * 8;
+    constexpr int kLdsQ = kLdsRaw + (kEarly ? kBtRaw * 4 : 0);
+    constexpr int kLdsBytes = kLdsQ + (kEarly ? 16 * NRB * 2 * kDim : 0);
     static_assert(kLdsBytes <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
     __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
 
@@ -376,9 +390,17 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     const int tid = threadIdx.x, l = tid & 63, lg = l >> 4, li = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, uniform by construction
 
+    // The set-up is a chain of dependent scalar loads (arguments, sequence, block table) before
+    // the first copy: make each link one round trip. Every argument the set-up reads is
+    // requested at once, then the three sequence words together.
+    asm volatile("" ::"s"(a.qsl), "s"(a.seq_lens), "s"(a.block_table), "s"(a.bt_stride), "s"(a.kc), "s"(a.k_sb),
+                 "s"(a.k_ss), "s"(a.k_sh), "s"(a.q), "s"(a.q_st), "s"(a.qmax), "s"(a.G), "s"(a.window),
+                 "s"(a.nsplit), "s"(a.block_size), "s"(a.bs_shift));
     const int q0 = a.qsl[b];
-    const int q_len = a.qsl[b + 1] - q0;
+    const int q_end = a.qsl[b + 1];
     const int seq_len = a.seq_lens[b];
+    asm volatile("" ::"s"(q0), "s"(q_end), "s"(seq_len));
+    const int q_len = q_end - q0;
     if (q_len <= 0 || seq_len <= 0) return;
     const int ql = min(q_len, a.qmax);
     const int G = a.G;
@@ -444,6 +466,7 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         rvalid[rb] = r < R;
         const int qi = r / G, qh = r - (r / G) * G;
         rpos[rb] = ctx0 + qi;
+        if constexpr (kEarly) continue;
         const _Float16* qrow =
             a.q + (int64_t)(q0 + (rvalid[rb] ? qi : 0)) * a.q_st + (int64_t)(g * G + (rvalid[rb] ? qh : 0)) * kDim;
 #pragma unroll
@@ -470,7 +493,63 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     }
 
     // ---- block-table slice of the split into LDS ----
-    {
+    if constexpr (kEarly) {
+        const int pk_first = max(tb * kTile, lo), pk_last = min(te * kTile, hi) - 1;
+        const int plast = pk_last / a.block_size;
+        const int npages = plast - pt.pfirst + 1;
+        const int nblk = 2 * (te - tb);
+        pt.in_lds = nblk <= kBtEarly && npages <= kBtRaw;
+        (void)pk_first;
+        // (1) Q rows (two 512-byte rows per copy; rows past R repeat row R - 1) and the raw
+        //     block-table entries [pfirst, plast], spread over the waves
+        const int nq = (R + 1) / 2;
+        for (int i = w; i < nq; i += kWaves) {
+            const int r = min(2 * i + (l >> 5), R - 1);
+            const int qi = r / G, qh = r - qi * G;
+            const _Float16* qrow = a.q + (int64_t)(q0 + qi) * a.q_st + (int64_t)(g * G + qh) * kDim;
+            dma16_v<0>(reinterpret_cast<const int8_t*>(qrow) + 16 * (l & 31), lds_base + (unsigned)(kLdsQ + 1024 * i));
+        }
+        if (pt.in_lds) {
+            const int* bt_glob = a.block_table + (int64_t)b * a.bt_stride;
+            for (int i = w; 64 * i < npages; i += kWaves)
+                dma4_v(bt_glob + min(pt.pfirst + 64 * i + l, plast), lds_base + (unsigned)(kLdsRaw + 256 * i));
+        }
+        // (2) this wave's first two tiles
+        if (nt > 0) issue_tile<kFast>(a, tile_src<kFast, false>(a, pt, gbase, tile_of(0), tb, lo, hi, l), dl, wslots, l);
+        if (nt > 1)
+            issue_tile<kFast>(a, tile_src<kFast, false>(a, pt, gbase, tile_of(1), tb, lo, hi, l), dl,
+                              wslots + (unsigned)kSlot, l);
+        // (3) wait for (1) only: the tile copies were issued after it
+        if (nt > 1)
+            wait_vm<34>();
+        else if (nt == 1)
+            wait_vm<17>();
+        else
+            wait_vm<0>();
+        __syncthreads();
+        if (pt.in_lds) {
+            const lds_int* raw = (const lds_int*)(L + kLdsRaw);
+            lds_u64* dst = (lds_u64*)(L + kLdsBt);
+            for (int i = tid; i < nblk; i += kThreads) {
+                const int kb = (tb + (i >> 1)) * kTile;
+                const int kfirst = max(kb, lo), klast = min(kb + kTile - 1, hi - 1);
+                const int key0 = min(max(kb + 16 * (i & 1), kfirst), klast) & ~15;
+                const int lb = key0 / a.block_size;
+                dst[i] = (uint64_t)((int64_t)raw[lb - pt.pfirst] * a.k_sb + (int64_t)(key0 - lb * a.block_size) * a.k_ss);
+            }
+        }
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) {
+            const lds_u8* qrow = L + kLdsQ + (16 * rb + li) * (2 * kDim);
+#pragma unroll
+            for (int st = 0; st < 8; ++st) {
+                const int dim = 64 * (st >> 1) + 16 * lg + 8 * (st & 1);
+                const half8_t v = *(const lds_half8*)(qrow + 2 * dim);
+                qop[rb][st] = rvalid[rb] ? v : (half8_t)(_Float16)0.0f;
+            }
+        }
+        __syncthreads();  // the block offsets are visible
+    } else {
         const int pk_first = max(tb * kTile, lo), pk_last = min(te * kTile, hi) - 1;
         const int* bt_glob = a.block_table + (int64_t)b * a.bt_stride;
         if constexpr (kFast) {
@@ -711,10 +790,13 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
             issue_tile<kFast>(a, tile_src<kFast, kLds>(a, pt, gbase, tile_of(n), tb, lo, hi, l), dl,
                               wslots + (unsigned)((n & 1) * kSlot), l);
         };
-        // The first two tiles: all loads the compiler can see (Q, block table) have been waited
-        // for by now, so no compiler-inserted wait will include these copies.
-        if (nt > 0) issue(0);
-        if (nt > 1) issue(1);
+        // The first two tiles (issued during the set-up when kEarly): all loads the compiler can
+        // see (Q, block table) have been waited for by now, so no compiler-inserted wait will
+        // include these copies.
+        if constexpr (!kEarly) {
+            if (nt > 0) issue(0);
+            if (nt > 1) issue(1);
+        }
         float sv[NRB][8];
         TileOps ops;
         bool interior = true;
@@ -1156,7 +1238,6 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
         for (int m = 0; m < 17; ++m) oacc[rb][m] = (float4_t)0.f;
     }
 
-    typedef __attribute__((address_space(3))) half8_t lds_half8;
     typedef __attribute__((address_space(3))) float4_t lds_float4;
     auto hbuf = [&](int n) __attribute__((always_inline)) { return L + kLdsH + (n & 1) * kFaHBuf; };
     auto raw = [&](int n) __attribute__((always_inline)) { return L + kLdsRaw + (n & (kFaRaw - 1)) * kSlot; };

@@ -63,12 +63,15 @@ class PdTensor(ctypes.Structure):
 
 
 _lib = None
+_lib_path = None
 
 
 def load_library(path: str | None = None) -> ctypes.CDLL:
-    """Load libpthdec.so (once) and declare the C signatures. Raises if it is not built."""
-    global _lib
-    if _lib is not None and path is None:
+    """Load libpthdec.so and declare the C signatures; raises if it is not built. The library
+    loaded last is the one every operator call uses: load_library() returns it (loading LIB_PATH
+    the first time), load_library(path) switches to `path`."""
+    global _lib, _lib_path
+    if _lib is not None and (path is None or os.path.realpath(path) == _lib_path):
         return _lib
     p = path or LIB_PATH
     if not os.path.exists(p):
@@ -102,8 +105,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.pth_cache_write.restype = c_int
     lib.pth_dec_version.argtypes = []
     lib.pth_dec_version.restype = ctypes.c_char_p
-    if path is None:
-        _lib = lib
+    _lib, _lib_path = lib, os.path.realpath(p)
     return lib
 
 

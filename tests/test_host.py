@@ -8,6 +8,7 @@ calls reaches a device: every case here fails validation or has no tokens.
 """
 import ctypes
 import os
+import shutil
 import re
 
 import pytest
@@ -30,6 +31,21 @@ def declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(pth_(?:dec|fa|cache)_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_load_library_switches_active_library(tmp_path):
+    """An explicitly loaded library (the vLLM shim's *_LIB switch) is the one later calls use."""
+    active = pth_dec.load_library()
+    copy = tmp_path / "libpthdec_copy.so"
+    shutil.copy(pth_dec.LIB_PATH, copy)
+    try:
+        other = pth_dec.load_library(str(copy))
+        assert other is not active
+        assert pth_dec.load_library() is other
+        assert pth_dec.load_library(str(copy)) is other
+    finally:
+        pth_dec.load_library(pth_dec.LIB_PATH)
+    assert pth_dec.load_library() is not other
 
 
 def test_header_symbols_exported(lib):
