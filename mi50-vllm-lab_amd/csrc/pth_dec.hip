@@ -376,8 +376,9 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     constexpr int kLdsMain = kLdsWaves > kLdsMerge ? kLdsWaves : kLdsMerge;
     constexpr int kLdsStats = kLdsMain;                   // m, l: [wave][NRB][16]
     // kEarly: Q and the block-table slice are copied into LDS like the tiles, and each wave's
-    // first two tiles are issued before anything is waited for (addressed with scalar
-    // block-table loads), so the copies start one memory round trip after the kernel does.
+    // first tile is issued before anything is waited for (addressed with scalar block-table
+    // loads), so the copies start one memory round trip after the kernel does; the second tile
+    // follows the set-up (a copy issue stalls while the memory queues are full).
     constexpr bool kEarly = kFast && NRB <= 2;
     constexpr int kLdsBt = kLdsStats + 2 * kWaves * NRB * 16 * 4;
     constexpr int kLdsRaw = kLdsBt + (kEarly ? kBtEarly : kBtCache) * 8;
@@ -500,6 +501,30 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         const int nblk = 2 * (te - tb);
         pt.in_lds = nblk <= kBtEarly && npages <= kBtRaw;
         (void)pk_first;
+        // (0) the block-table entries of this wave's first two tiles (scalar loads), requested
+        //     before any copy so that they do not queue behind the kernel's first copies
+        //     (all four entries in one round trip; the tile_src rule, keys clamped into the tile's
+        //     visible range, which also keeps the entries of a missing tile in bounds)
+        int key0[4], lb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int kb = tile_of(i >> 1) * kTile;
+            const int kfirst = max(kb, lo), klast = min(kb + kTile - 1, hi - 1);
+            key0[i] = min(max(kb + 16 * (i & 1), kfirst), klast) & ~15;
+            lb[i] = a.bs_shift >= 0 ? key0[i] >> a.bs_shift : key0[i] / a.block_size;
+        }
+        int ent[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ent[i] = pt.glob[lb[i]];
+        TileSrc src0, src1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int8_t* base = gbase + (int64_t)ent[i] * a.k_sb + (int64_t)(key0[i] - lb[i] * a.block_size) * a.k_ss;
+            if (i < 2)
+                src0.base[i] = base;
+            else
+                src1.base[i - 2] = base;
+        }
         // (1) Q rows (two 512-byte rows per copy; rows past R repeat row R - 1) and the raw
         //     block-table entries [pfirst, plast], spread over the waves
         const int nq = (R + 1) / 2;
@@ -514,15 +539,10 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
             for (int i = w; 64 * i < npages; i += kWaves)
                 dma4_v(bt_glob + min(pt.pfirst + 64 * i + l, plast), lds_base + (unsigned)(kLdsRaw + 256 * i));
         }
-        // (2) this wave's first two tiles
-        if (nt > 0) issue_tile<kFast>(a, tile_src<kFast, false>(a, pt, gbase, tile_of(0), tb, lo, hi, l), dl, wslots, l);
-        if (nt > 1)
-            issue_tile<kFast>(a, tile_src<kFast, false>(a, pt, gbase, tile_of(1), tb, lo, hi, l), dl,
-                              wslots + (unsigned)kSlot, l);
-        // (3) wait for (1) only: the tile copies were issued after it
-        if (nt > 1)
-            wait_vm<34>();
-        else if (nt == 1)
+        // (2) this wave's first tile; its second tile is issued once the set-up below is done
+        if (nt > 0) issue_tile<kFast>(a, src0, dl, wslots, l);
+        // (3) wait for (1) only
+        if (nt > 0)
             wait_vm<17>();
         else
             wait_vm<0>();
@@ -549,6 +569,7 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
             }
         }
         __syncthreads();  // the block offsets are visible
+        if (nt > 1) issue_tile<kFast>(a, src1, dl, wslots + (unsigned)kSlot, l);
     } else {
         const int pk_first = max(tb * kTile, lo), pk_last = min(te * kTile, hi) - 1;
         const int* bt_glob = a.block_table + (int64_t)b * a.bt_stride;
