@@ -383,7 +383,12 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     constexpr int kLdsBt = kLdsStats + 2 * kWaves * NRB * 16 * 4;
     constexpr int kLdsRaw = kLdsBt + (kEarly ? kBtEarly : kBtCache) * 8;
     constexpr int kLdsQ = kLdsRaw + (kEarly ? kBtRaw * 4 : 0);
-    constexpr int kLdsBytes = kLdsQ + (kEarly ? 16 * NRB * 2 * kDim : 0);
+    // NRB <= 2: the merge's per-row tables reuse the Q region (or follow the block table)
+    constexpr int kQBytes = kEarly ? 16 * NRB * 2 * kDim : 0;
+    constexpr int kMergeCBytes = NRB <= 2 ? (2 * kWaves + 1) * NRB * 16 * 4 + NRB * 16 * 8 : 0;
+    constexpr int kLdsMergeC = kLdsQ;
+    constexpr int kLdsBytes = kLdsQ + (kQBytes > kMergeCBytes ? kQBytes : kMergeCBytes);
+    static_assert(NRB > 2 || kWaves * NRB * 17 * 1024 <= kLdsWaves, "accumulator blocks fit the slots");
     static_assert(kLdsBytes <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
     __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
 
@@ -858,6 +863,85 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         tile_loop(std::false_type{});
 
     // ---- merge the waves through LDS and write one partial per row ----
+    if constexpr (NRB <= 2) {
+        // Each wave stores its accumulators as they are (a 1 KiB block per accumulator and row
+        // block, straight from the AGPRs: no vector ALU work) with its per-row max, sum and
+        // V widening bias; one pass turns those into per-row factors; then thread (row, 32 dims)
+        // sums the four waves' blocks with the factors and writes the partial row.
+        float* wm = reinterpret_cast<float*>(lds + kLdsStats);  // [wave][NRB][16] running max
+        float* wl = wm + kWaves * NRB * 16;                     // [wave][NRB][16] row sum of p
+        float* wc = reinterpret_cast<float*>(lds + kLdsMergeC);  // [wave][NRB][16] 1152 sum P'
+        float* rf = wc + kWaves * NRB * 16;                     // [wave][NRB * 16] factor of O
+        float* rc = rf + kWaves * NRB * 16;                     // [NRB * 16] sum_w factor * bias
+        int64_t* ro = reinterpret_cast<int64_t*>(rc + NRB * 16);  // [NRB * 16] partial row offset
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) {
+            const float l_row = xor_sum(xor_sum(l_run[rb], 16), 32);
+            const float cr = __shfl(oacc[rb][16].x, 48 + li, 64);  // 1152 * sum of the row's P'
+            if (lg == 0) {
+                wm[(w * NRB + rb) * 16 + li] = m_run[rb];
+                wl[(w * NRB + rb) * 16 + li] = l_row;
+                wc[(w * NRB + rb) * 16 + li] = cr;
+            }
+        }
+        wait_lds();
+        __syncthreads();  // every wave is done with its slots: the accumulator blocks alias them
+        const unsigned raw = lds_base + (unsigned)(w * NRB * 17 * 1024 + 16 * l);
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+            for (int m = 0; m < 17; ++m)
+                asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(raw), "a"(oacc[rb][m]), "i"((rb * 17 + m) * 1024)
+                             : "memory");
+        if (tid < NRB * 16) {  // row tid: M = max_w m_w, e_w = 2^(m_w - M), L = sum_w e_w l_w
+            float M = kNegInf;
+#pragma unroll
+            for (int v = 0; v < kWaves; ++v) M = fmaxf(M, wm[v * NRB * 16 + tid]);
+            float Lr = 0.f, C = 0.f;
+#pragma unroll
+            for (int v = 0; v < kWaves; ++v) {
+                const float mw = wm[v * NRB * 16 + tid];
+                const float e = mw == kNegInf ? 0.f : exp2f(mw - M);
+                Lr += e * wl[v * NRB * 16 + tid];
+                rf[v * NRB * 16 + tid] = e * (1.0f / kPScale);
+                C += e * (1.0f / kPScale) * wc[v * NRB * 16 + tid];
+            }
+            rc[tid] = C;
+            if (tid < R) {
+                const int64_t pr = prow(tid);
+                ro[tid] = pr * kDim;
+                a.part_m[pr] = M;
+                a.part_l[pr] = Lr;
+            }
+        }
+        wait_lds();
+        __syncthreads();
+        // thread: row = lane & 31 of wave w's two 32-dim parts; dims d of an accumulator block:
+        // block m < 16 holds 16 m - 4 + 4 lg .. + 3 in lane group lg, block 16 holds 252..255 in
+        // lane group 2
+        const int row = l & 31, part = 2 * w + (l >> 5);
+        if (row < R) {
+            const int rbo = row >> 4;
+            float f[kWaves];
+#pragma unroll
+            for (int v = 0; v < kWaves; ++v) f[v] = rf[v * NRB * 16 + row];
+            const float C = rc[row];
+            float* dst = a.part_o + ro[row];
+            const float4_t* rawp = reinterpret_cast<const float4_t*>(lds);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int d = 32 * part + 4 * j;
+                const int m = d < 252 ? (d + 4) >> 4 : 16;
+                const int glg = d < 252 ? ((d + 4) >> 2) & 3 : 2;
+                const int blk = (rbo * 17 + m) * 64 + 16 * glg + (row & 15);
+                float4_t acc = (float4_t)(-C);
+#pragma unroll
+                for (int v = 0; v < kWaves; ++v) acc += rawp[v * NRB * 17 * 64 + blk] * f[v];
+                *reinterpret_cast<float4_t*>(dst + d) = acc;
+            }
+        }
+        return;
+    }
     float* wm = reinterpret_cast<float*>(lds + kLdsStats);  // [wave][NRB][16]
     float* wl = wm + kWaves * NRB * 16;
     float corr[NRB];
