@@ -155,6 +155,28 @@ def test_row_counts_and_masks(qlen, window, causal):
         assert emax <= 2e-3 and emean <= 2e-4, (ns, emax, emean)
 
 
+@pytest.mark.parametrize("hq,hkv,qlens", [(8, 8, [4, 4]), (16, 8, [4, 3]), (12, 4, [4]), (20, 4, [3, 1]),
+                                            (32, 4, [4]), (48, 1, [1])])
+def test_gqa_group_sizes(hq, hkv, qlens):
+    """Rows per kv head R = qmax * G from 4 to 48 (one, two and three row blocks) and the row ->
+    (token, head) mapping for G = 1 .. 48; the reference only ran G = 6."""
+    c = kvc.make_case([2500, 700][:len(qlens)], qlens, num_q_heads=hq, num_kv_heads=hkv, block_size=16,
+                      seed=hq * 7 + hkv)
+    ref, written = oracle_of(c)
+    d = c.to("cuda")
+    for ns in (1, 9):
+        say(f"gqa hq={hq} hkv={hkv} qlens={qlens} nsplit={ns}")
+        T = d.num_tokens
+        out = torch.full((T, hq, 256), float("nan"), dtype=torch.float16, device="cuda")
+        po, pm, pl = kvc.partial_buffers(T, hq, NSEG, "cuda")
+        pth_dec.decode(d.q, d.cache.key_cache, d.cache.value_cache, d.cache.k_scale, d.cache.v_scale, d.block_table,
+                       d.seq_lens, d.query_start_loc, out, d.scale, po, pm, pl, d.num_seqs, d.qmax, ns, d.window,
+                       d.causal)
+        torch.cuda.synchronize()
+        emax, emean = errors(out, ref, written)
+        assert emax <= 2e-3 and emean <= 2e-4, (ns, emax, emean)
+
+
 def test_padding_tokens_untouched():
     c = kvc.make_case([300, 40], [4, 2], num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=8)
     d = c.to("cuda")

@@ -102,6 +102,19 @@ def test_batches_with_chunk_offsets(bs, layout):
     assert (out.cpu().numpy()[~written] == 0).all()  # rows that see no key are written as 0
 
 
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (32, 4), (28, 4), (48, 2)])
+def test_gqa_group_sizes(hq, hkv):
+    """G = 1, 8, 7 (192 rows per workgroup is not a multiple of 7: 27 tokens) and 24."""
+    c = kvc.make_case([900, 40], [77, 77], num_q_heads=hq, num_kv_heads=hkv, block_size=16, seed=hq + 5 * hkv)
+    q_abs = [900, 10]
+    say(f"prefill gqa hq={hq} hkv={hkv}")
+    out = gpu_prefill(c.to("cuda"), q_abs)
+    ref, written = oracle_of(c, q_abs)
+    emax, emean = errors(out, ref, written)
+    say(f"  max-abs {emax:.2e} mean-abs {emean:.2e}")
+    assert emax <= 2e-3 and emean <= 2e-4, (emax, emean)
+
+
 def abs_value_case(c):
     """The case with every V quant replaced by its absolute value. The quantised rows hold
     [-127, 127]; only unused slots (never read) can hold -128."""
