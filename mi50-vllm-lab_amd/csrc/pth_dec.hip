@@ -12,13 +12,15 @@
 //   DFlash2) are held as 16-row blocks, so one read of a K/V tile serves every row.
 //
 // Memory path: HBM -> LDS by DMA (global_load_lds_dwordx4), double-buffered per wave, no VGPR
-//   holding data in flight. One DMA instruction moves two whole key rows (lanes 0-31: bytes
-//   [0, 512) of row 2i, lanes 32-63: of row 2i+1; 512 contiguous bytes per half-wave), 16
-//   instructions per tile plus one for bytes [504, 520) of each row. With block_size 16 or
-//   >= 32 (even) both rows of a pair sit in one page, so every instruction is addressed by a
-//   scalar base (page, slot: scalar ALU) and a per-lane constant offset: no vector ALU per DMA.
-//   The next tile's DMAs are issued before the current tile is computed; s_waitcnt vmcnt
-//   waits for the current one only. The block-table slice of the split is staged in LDS once.
+//   holding data in flight. A tile is 17 DMA instructions of 1 KiB: 8 for K (4 rows x 256
+//   bytes each, at positions swizzled so the operand reads are bank-conflict free), 8 for
+//   bytes [256, 512) of the rows (k_scale and V), one for bytes [504, 520) (the last V bytes and
+//   v_scale). With block_size a multiple of 16 a 16-key row block sits in one page, so each
+//   instruction is a scalar base (page, slot) plus a per-lane constant offset. Tile n + 1 is in
+//   flight while tile n is computed; tile n + 2 is issued into tile n's slot once tile n is
+//   done. The block-table slice of the split is staged in LDS once (as 64-bit row offsets), and
+//   with one or two row blocks Q is copied into LDS the same way, so the first tile is issued
+//   one memory round trip after the kernel starts.
 //
 // Per 32-key tile, per wave
 //   S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims of K (int8 widened to fp16
@@ -39,8 +41,13 @@
 //
 // End of split: the 4 waves merge (m, l, O) through LDS and write one partial per row:
 //   part_o [T, Hq, nseg, 256] unnormalised, part_m [T, Hq, nseg] running max in log2 units,
-//   part_l the matching sum. Splits with no tiles write m = -inf. The combine kernel
-//   merges the partials of each (token, head) with a log-sum-exp rescale.
+//   part_l the matching sum. With one or two row blocks each wave stores its accumulators
+//   straight from the AGPRs and the per-row factors are applied while summing. Splits with no
+//   tiles write m = -inf. The combine kernel merges the partials of each (token, head) with a
+//   log-sum-exp rescale.
+//
+// The file also holds the chunked-prefill kernel (same cache, same tile copies, 192 rows per
+// workgroup) and the KV-cache writer; each has its own description below.
 //
 // Nothing is allocated, nothing waits for the host, and every split range is derived on
 // the device from seq_lens / query_start_loc, so launches can be captured in a HIP graph.
