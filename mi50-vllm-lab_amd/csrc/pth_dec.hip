@@ -1055,16 +1055,18 @@ __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) 
         ov[i] = ok ? po[(int64_t)sgi * (kDim / 4)] : (float4_t)0.f;
     }
 
-    // sequence of this token = number of sequences whose query rows end at or before it
+    // sequence of this token = number of sequences whose query rows end at or before it; the
+    // lookup only gates the final store, so its loads overlap the merge (the merge of a padding
+    // token reads allocated but unwritten partials and is discarded)
     int b = 0;
     for (int i0 = 0; i0 < a.num_seqs; i0 += 64) {
         const int i = i0 + lane + 1;
         const bool ended = i <= a.num_seqs && a.qsl[i] <= tok;
         b += __popcll(__ballot(ended));
     }
-    if (b >= a.num_seqs || tok < a.qsl[b]) return;  // padding token
-    if (a.seq_lens[b] <= 0) return;
-    if (tok - a.qsl[b] >= a.qmax) return;  // rows past qmax are not computed
+    const int bq = min(b, a.num_seqs - 1);
+    const int q_b = a.qsl[bq], len_b = a.seq_lens[bq];
+    const bool live = b < a.num_seqs && tok >= q_b && len_b > 0 && tok - q_b < a.qmax;
     float mx = kNegInf;
 #pragma unroll
     for (int i = 0; i < kCombPer; ++i) mx = fmaxf(mx, mv[i]);
@@ -1104,7 +1106,7 @@ __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) 
     if (lane < 16) s_acc[wave][lane] = acc;
     if (lane == 0) s_l[wave] = lsum;
     __syncthreads();
-    if (tid < 16) {
+    if (live && tid < 16) {
         const float4_t r = s_acc[0][tid] + s_acc[1][tid] + s_acc[2][tid] + s_acc[3][tid];
         const float L = s_l[0] + s_l[1] + s_l[2] + s_l[3];
         const float inv = L > 0.f ? 1.f / L : 0.f;
