@@ -126,7 +126,7 @@ def test_nan_poisoned_freed_pages_bit_exact():
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
-@pytest.mark.parametrize("bs", [16, 1584, 8, 1])
+@pytest.mark.parametrize("bs", [16, 32, 64, 1584, 8, 1])
 def test_physical_layout_bit_exact(bs):
     args = dict(num_q_heads=HQ, num_kv_heads=HKV, block_size=bs, seed=77)
     ctxs, qlens = ([3000, 517], [4, 3]) if bs > 1 else ([700, 90], [4, 3])
