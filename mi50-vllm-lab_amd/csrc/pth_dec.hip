@@ -108,7 +108,6 @@ constexpr int kSlot = kImgT + 1024;
 constexpr int kWaveLds = 2 * kSlot;                // LDS bytes per wave
 constexpr int kWaves = 4;                          // independent tile streams per workgroup
 constexpr int kThreads = 64 * kWaves;
-constexpr int kOPitch = kDim + 4;                  // floats per row of the merge buffer
 constexpr int kBtCache = 1024;                     // block-table entries of a split kept in LDS
 // With Q staged in LDS as well (one or two row blocks) the block-table slice is smaller:
 constexpr int kBtEarly = 384;                      // per-block row offsets (192 tiles per split)
@@ -378,10 +377,7 @@ __device__ __forceinline__ void agpr_scale_via_lds(float4_t& acc, float alpha, u
 template <int NRB, bool kFast>
 __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialParams a) {
     constexpr int kLdsWaves = kWaves * kWaveLds;
-    constexpr int kMergeRows = NRB <= 2 ? 16 * NRB : 16;  // rows merged per round
-    constexpr int kLdsMerge = kWaves * kMergeRows * kOPitch * 4;
-    constexpr int kLdsMain = kLdsWaves > kLdsMerge ? kLdsWaves : kLdsMerge;
-    constexpr int kLdsStats = kLdsMain;                   // m, l: [wave][NRB][16]
+    constexpr int kLdsStats = kLdsWaves;                  // m, l: [wave][NRB][16]
     // kEarly: Q and the block-table slice are copied into LDS like the tiles, and each wave's
     // first tile is issued before anything is waited for (addressed with scalar block-table
     // loads), so the copies start one memory round trip after the kernel does; the second tile
@@ -392,10 +388,10 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     constexpr int kLdsQ = kLdsRaw + (kEarly ? kBtRaw * 4 : 0);
     // NRB <= 2: the merge's per-row tables reuse the Q region (or follow the block table)
     constexpr int kQBytes = kEarly ? 16 * NRB * 2 * kDim : 0;
-    constexpr int kMergeCBytes = NRB <= 2 ? (2 * kWaves + 1) * NRB * 16 * 4 + NRB * 16 * 8 : 0;
+    constexpr int kMergeCBytes = (2 * kWaves + 1) * NRB * 16 * 4 + NRB * 16 * 8;
     constexpr int kLdsMergeC = kLdsQ;
     constexpr int kLdsBytes = kLdsQ + (kQBytes > kMergeCBytes ? kQBytes : kMergeCBytes);
-    static_assert(NRB > 2 || kWaves * NRB * 17 * 1024 <= kLdsWaves, "accumulator blocks fit the slots");
+    static_assert(kWaves * 2 * 17 * 1024 <= kLdsWaves, "two row blocks of accumulator blocks fit the slots");
     static_assert(kLdsBytes <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
     __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
 
@@ -870,11 +866,13 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         tile_loop(std::false_type{});
 
     // ---- merge the waves through LDS and write one partial per row ----
-    if constexpr (NRB <= 2) {
+    {
         // Each wave stores its accumulators as they are (a 1 KiB block per accumulator and row
         // block, straight from the AGPRs: no vector ALU work) with its per-row max, sum and
         // V widening bias; one pass turns those into per-row factors; then thread (row, 32 dims)
-        // sums the four waves' blocks with the factors and writes the partial row.
+        // sums the four waves' blocks with the factors and writes the partial row. Row blocks go
+        // through the slots two at a time (kRawRounds rounds).
+        constexpr int kRawRounds = (NRB + 1) / 2;
         float* wm = reinterpret_cast<float*>(lds + kLdsStats);  // [wave][NRB][16] running max
         float* wl = wm + kWaves * NRB * 16;                     // [wave][NRB][16] row sum of p
         float* wc = reinterpret_cast<float*>(lds + kLdsMergeC);  // [wave][NRB][16] 1152 sum P'
@@ -893,125 +891,65 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         }
         wait_lds();
         __syncthreads();  // every wave is done with its slots: the accumulator blocks alias them
-        const unsigned raw = lds_base + (unsigned)(w * NRB * 17 * 1024 + 16 * l);
+        const unsigned raw = lds_base + (unsigned)(w * 2 * 17 * 1024 + 16 * l);
 #pragma unroll
-        for (int rb = 0; rb < NRB; ++rb)
+        for (int rd = 0; rd < kRawRounds; ++rd) {
 #pragma unroll
-            for (int m = 0; m < 17; ++m)
-                asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(raw), "a"(oacc[rb][m]), "i"((rb * 17 + m) * 1024)
-                             : "memory");
-        if (tid < NRB * 16) {  // row tid: M = max_w m_w, e_w = 2^(m_w - M), L = sum_w e_w l_w
-            float M = kNegInf;
+            for (int rb = 2 * rd; rb < 2 * rd + 2 && rb < NRB; ++rb)
 #pragma unroll
-            for (int v = 0; v < kWaves; ++v) M = fmaxf(M, wm[v * NRB * 16 + tid]);
-            float Lr = 0.f, C = 0.f;
+                for (int m = 0; m < 17; ++m)
+                    asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(raw), "a"(oacc[rb][m]),
+                                 "i"(((rb - 2 * rd) * 17 + m) * 1024)
+                                 : "memory");
+            if (rd == 0 && tid < NRB * 16) {  // row tid: M = max_w m_w, e_w = 2^(m_w - M), L = sum_w e_w l_w
+                float M = kNegInf;
 #pragma unroll
-            for (int v = 0; v < kWaves; ++v) {
-                const float mw = wm[v * NRB * 16 + tid];
-                const float e = mw == kNegInf ? 0.f : exp2f(mw - M);
-                Lr += e * wl[v * NRB * 16 + tid];
-                rf[v * NRB * 16 + tid] = e * (1.0f / kPScale);
-                C += e * (1.0f / kPScale) * wc[v * NRB * 16 + tid];
-            }
-            rc[tid] = C;
-            if (tid < R) {
-                const int64_t pr = prow(tid);
-                ro[tid] = pr * kDim;
-                a.part_m[pr] = M;
-                a.part_l[pr] = Lr;
-            }
-        }
-        wait_lds();
-        __syncthreads();
-        // thread: row = lane & 31 of wave w's two 32-dim parts; dims d of an accumulator block:
-        // block m < 16 holds 16 m - 4 + 4 lg .. + 3 in lane group lg, block 16 holds 252..255 in
-        // lane group 2
-        const int row = l & 31, part = 2 * w + (l >> 5);
-        if (row < R) {
-            const int rbo = row >> 4;
-            float f[kWaves];
-#pragma unroll
-            for (int v = 0; v < kWaves; ++v) f[v] = rf[v * NRB * 16 + row];
-            const float C = rc[row];
-            float* dst = a.part_o + ro[row];
-            const float4_t* rawp = reinterpret_cast<const float4_t*>(lds);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int d = 32 * part + 4 * j;
-                const int m = d < 252 ? (d + 4) >> 4 : 16;
-                const int glg = d < 252 ? ((d + 4) >> 2) & 3 : 2;
-                const int blk = (rbo * 17 + m) * 64 + 16 * glg + (row & 15);
-                float4_t acc = (float4_t)(-C);
-#pragma unroll
-                for (int v = 0; v < kWaves; ++v) acc += rawp[v * NRB * 17 * 64 + blk] * f[v];
-                *reinterpret_cast<float4_t*>(dst + d) = acc;
-            }
-        }
-        return;
-    }
-    float* wm = reinterpret_cast<float*>(lds + kLdsStats);  // [wave][NRB][16]
-    float* wl = wm + kWaves * NRB * 16;
-    float corr[NRB];
-#pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) {
-        const float l_row = xor_sum(xor_sum(l_run[rb], 16), 32);
-        corr[rb] = __shfl(oacc[rb][16].x, 48 + li, 64);  // 1152 * sum of the row's P'
-        if (lg == 0) {
-            wm[(w * NRB + rb) * 16 + li] = m_run[rb];
-            wl[(w * NRB + rb) * 16 + li] = l_row;
-        }
-    }
-    __syncthreads();  // stats visible; every wave is done with its slots (the slab aliases them)
-    float* slab = reinterpret_cast<float*>(lds);  // [wave][kMergeRows][kOPitch]
-    constexpr int kRounds = NRB * 16 / kMergeRows;
-    constexpr int kRbPerRound = kMergeRows / 16;
-#pragma unroll
-    for (int rd = 0; rd < kRounds; ++rd) {
-#pragma unroll
-        for (int k = 0; k < kRbPerRound; ++k) {
-            const int rb = rd * kRbPerRound + k;
-            float M = kNegInf;
-#pragma unroll
-            for (int v = 0; v < kWaves; ++v) M = fmaxf(M, wm[(v * NRB + rb) * 16 + li]);
-            const float f = m_run[rb] == kNegInf ? 0.f : exp2f(m_run[rb] - M) * (1.0f / kPScale);
-            float* ob = slab + (w * kMergeRows + 16 * k + li) * kOPitch;
-#pragma unroll
-            for (int m = 0; m < 17; ++m) {
-                const int d0 = m < 16 ? 16 * m - 4 + 4 * lg : (lg == 2 ? 252 : -1);
-                if (d0 >= 0 && d0 < kDim) *reinterpret_cast<float4_t*>(ob + d0) = (oacc[rb][m] - corr[rb]) * f;
-            }
-        }
-        __syncthreads();
-        // thread -> (row of the round, 16 * kRbPerRound dims)
-        constexpr int kDimsPerThread = 16 * kRbPerRound;
-        const int orow = tid / (kDim / kDimsPerThread), dq = (tid % (kDim / kDimsPerThread)) * kDimsPerThread;
-        const int rr = rd * kMergeRows + orow;
-        if (orow < kMergeRows && rr < R) {
-            float* dst = a.part_o + prow(rr) * kDim + dq;
-#pragma unroll
-            for (int q4 = 0; q4 < kDimsPerThread / 4; ++q4) {
-                float4_t acc = (float4_t)0.f;
-#pragma unroll
-                for (int v = 0; v < kWaves; ++v)
-                    acc += *reinterpret_cast<const float4_t*>(slab + (v * kMergeRows + orow) * kOPitch + dq + 4 * q4);
-                *reinterpret_cast<float4_t*>(dst + 4 * q4) = acc;
-            }
-            if (dq == 0) {
-                const int rbo = rr >> 4, ro = rr & 15;
-                float Mr = kNegInf;
-#pragma unroll
-                for (int v = 0; v < kWaves; ++v) Mr = fmaxf(Mr, wm[(v * NRB + rbo) * 16 + ro]);
-                float Lr = 0.f;
+                for (int v = 0; v < kWaves; ++v) M = fmaxf(M, wm[v * NRB * 16 + tid]);
+                float Lr = 0.f, C = 0.f;
 #pragma unroll
                 for (int v = 0; v < kWaves; ++v) {
-                    const float mw = wm[(v * NRB + rbo) * 16 + ro];
-                    if (mw != kNegInf) Lr += exp2f(mw - Mr) * wl[(v * NRB + rbo) * 16 + ro];
+                    const float mw = wm[v * NRB * 16 + tid];
+                    const float e = mw == kNegInf ? 0.f : exp2f(mw - M);
+                    Lr += e * wl[v * NRB * 16 + tid];
+                    rf[v * NRB * 16 + tid] = e * (1.0f / kPScale);
+                    C += e * (1.0f / kPScale) * wc[v * NRB * 16 + tid];
                 }
-                a.part_m[prow(rr)] = Mr;
-                a.part_l[prow(rr)] = Lr;
+                rc[tid] = C;
+                if (tid < R) {
+                    const int64_t pr = prow(tid);
+                    ro[tid] = pr * kDim;
+                    a.part_m[pr] = M;
+                    a.part_l[pr] = Lr;
+                }
             }
+            wait_lds();
+            __syncthreads();
+            // thread: row 32 rd + (lane & 31), wave w's two 32-dim parts; dims d of an
+            // accumulator block: block m < 16 holds 16 m - 4 + 4 lg .. + 3 in lane group lg,
+            // block 16 holds 252..255 in lane group 2
+            const int row = 32 * rd + (l & 31), part = 2 * w + (l >> 5);
+            if (row < R) {
+                const int rbl = (row >> 4) - 2 * rd;  // row block within the round
+                float f[kWaves];
+#pragma unroll
+                for (int v = 0; v < kWaves; ++v) f[v] = rf[v * NRB * 16 + row];
+                const float C = rc[row];
+                float* dst = a.part_o + ro[row];
+                const float4_t* rawp = reinterpret_cast<const float4_t*>(lds);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int d = 32 * part + 4 * j;
+                    const int m = d < 252 ? (d + 4) >> 4 : 16;
+                    const int glg = d < 252 ? ((d + 4) >> 2) & 3 : 2;
+                    const int blk = (rbl * 17 + m) * 64 + 16 * glg + (row & 15);
+                    float4_t acc = (float4_t)(-C);
+#pragma unroll
+                    for (int v = 0; v < kWaves; ++v) acc += rawp[v * 2 * 17 * 64 + blk] * f[v];
+                    *reinterpret_cast<float4_t*>(dst + d) = acc;
+                }
+            }
+            if (rd + 1 < kRawRounds) __syncthreads();  // the blocks are rewritten for the next round
         }
-        if (rd + 1 < kRounds) __syncthreads();  // the slab is rewritten for the next round
     }
 }
 
