@@ -386,12 +386,13 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     constexpr int kLdsBt = kLdsStats + 2 * kWaves * NRB * 16 * 4;
     constexpr int kLdsRaw = kLdsBt + (kEarly ? kBtEarly : kBtCache) * 8;
     constexpr int kLdsQ = kLdsRaw + (kEarly ? kBtRaw * 4 : 0);
-    // NRB <= 2: the merge's per-row tables reuse the Q region (or follow the block table)
+    // the merge's table of V widening biases reuses the Q region (or follows the block table)
     constexpr int kQBytes = kEarly ? 16 * NRB * 2 * kDim : 0;
-    constexpr int kMergeCBytes = (2 * kWaves + 1) * NRB * 16 * 4 + NRB * 16 * 8;
+    constexpr int kMergeCBytes = kWaves * NRB * 16 * 4;
     constexpr int kLdsMergeC = kLdsQ;
     constexpr int kLdsBytes = kLdsQ + (kQBytes > kMergeCBytes ? kQBytes : kMergeCBytes);
-    static_assert(kWaves * 2 * 17 * 1024 <= kLdsWaves, "two row blocks of accumulator blocks fit the slots");
+    static_assert(2 * 17 * 1024 <= kWaveLds && kWaveLds % 16 == 0,
+                  "two row blocks of accumulator blocks fit the slots of their wave");
     static_assert(kLdsBytes <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
     __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
 
@@ -868,17 +869,15 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     // ---- merge the waves through LDS and write one partial per row ----
     {
         // Each wave stores its accumulators as they are (a 1 KiB block per accumulator and row
-        // block, straight from the AGPRs: no vector ALU work) with its per-row max, sum and
-        // V widening bias; one pass turns those into per-row factors; then thread (row, 32 dims)
-        // sums the four waves' blocks with the factors and writes the partial row. Row blocks go
-        // through the slots two at a time (kRawRounds rounds).
+        // block, straight from the AGPRs: no vector ALU work) into its own slots as soon as its
+        // tiles are done, with its per-row max, sum and V widening bias; then thread (row, 32
+        // dims) derives the wave factors of its row, sums the four waves' blocks with them and
+        // writes the partial row. Row blocks go through the slots two at a time (kRawRounds
+        // rounds).
         constexpr int kRawRounds = (NRB + 1) / 2;
         float* wm = reinterpret_cast<float*>(lds + kLdsStats);  // [wave][NRB][16] running max
         float* wl = wm + kWaves * NRB * 16;                     // [wave][NRB][16] row sum of p
         float* wc = reinterpret_cast<float*>(lds + kLdsMergeC);  // [wave][NRB][16] 1152 sum P'
-        float* rf = wc + kWaves * NRB * 16;                     // [wave][NRB * 16] factor of O
-        float* rc = rf + kWaves * NRB * 16;                     // [NRB * 16] sum_w factor * bias
-        int64_t* ro = reinterpret_cast<int64_t*>(rc + NRB * 16);  // [NRB * 16] partial row offset
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) {
             const float l_row = xor_sum(xor_sum(l_run[rb], 16), 32);
@@ -889,11 +888,8 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
                 wc[(w * NRB + rb) * 16 + li] = cr;
             }
         }
-        wait_lds();
-        __syncthreads();  // every wave is done with its slots: the accumulator blocks alias them
-        const unsigned raw = lds_base + (unsigned)(w * 2 * 17 * 1024 + 16 * l);
-#pragma unroll
-        for (int rd = 0; rd < kRawRounds; ++rd) {
+        const unsigned raw = lds_base + (unsigned)(w * kWaveLds + 16 * l);  // this wave's slots
+        auto store_round = [&](int rd) __attribute__((always_inline)) {
 #pragma unroll
             for (int rb = 2 * rd; rb < 2 * rd + 2 && rb < NRB; ++rb)
 #pragma unroll
@@ -901,40 +897,42 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
                     asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(raw), "a"(oacc[rb][m]),
                                  "i"(((rb - 2 * rd) * 17 + m) * 1024)
                                  : "memory");
-            if (rd == 0 && tid < NRB * 16) {  // row tid: M = max_w m_w, e_w = 2^(m_w - M), L = sum_w e_w l_w
+        };
+        store_round(0);
+        wait_lds();
+        __syncthreads();  // every wave's stats and first accumulator blocks are in LDS
+#pragma unroll
+        for (int rd = 0; rd < kRawRounds; ++rd) {
+            if (rd > 0) {
+                store_round(rd);
+                wait_lds();
+                __syncthreads();
+            }
+            // thread: row 32 rd + (lane & 31), wave w's two 32-dim parts. Row factors: M =
+            // max_w m_w, e_w = 2^(m_w - M), O = sum_w e_w O_w / 16 - sum_w e_w C_w / 16, L =
+            // sum_w e_w l_w. Dims d of an accumulator block: block m < 16 holds 16 m - 4 + 4 lg
+            // .. + 3 in lane group lg, block 16 holds 252..255 in lane group 2
+            const int row = 32 * rd + (l & 31), part = 2 * w + (l >> 5);
+            if (row < R) {
                 float M = kNegInf;
 #pragma unroll
-                for (int v = 0; v < kWaves; ++v) M = fmaxf(M, wm[v * NRB * 16 + tid]);
-                float Lr = 0.f, C = 0.f;
+                for (int v = 0; v < kWaves; ++v) M = fmaxf(M, wm[v * NRB * 16 + row]);
+                float f[kWaves], C = 0.f, Lr = 0.f;
 #pragma unroll
                 for (int v = 0; v < kWaves; ++v) {
-                    const float mw = wm[v * NRB * 16 + tid];
+                    const float mw = wm[v * NRB * 16 + row];
                     const float e = mw == kNegInf ? 0.f : exp2f(mw - M);
-                    Lr += e * wl[v * NRB * 16 + tid];
-                    rf[v * NRB * 16 + tid] = e * (1.0f / kPScale);
-                    C += e * (1.0f / kPScale) * wc[v * NRB * 16 + tid];
+                    f[v] = e * (1.0f / kPScale);
+                    C += f[v] * wc[v * NRB * 16 + row];
+                    Lr += e * wl[v * NRB * 16 + row];
                 }
-                rc[tid] = C;
-                if (tid < R) {
-                    const int64_t pr = prow(tid);
-                    ro[tid] = pr * kDim;
+                const int64_t pr = prow(row);
+                if (part == 0) {
                     a.part_m[pr] = M;
                     a.part_l[pr] = Lr;
                 }
-            }
-            wait_lds();
-            __syncthreads();
-            // thread: row 32 rd + (lane & 31), wave w's two 32-dim parts; dims d of an
-            // accumulator block: block m < 16 holds 16 m - 4 + 4 lg .. + 3 in lane group lg,
-            // block 16 holds 252..255 in lane group 2
-            const int row = 32 * rd + (l & 31), part = 2 * w + (l >> 5);
-            if (row < R) {
                 const int rbl = (row >> 4) - 2 * rd;  // row block within the round
-                float f[kWaves];
-#pragma unroll
-                for (int v = 0; v < kWaves; ++v) f[v] = rf[v * NRB * 16 + row];
-                const float C = rc[row];
-                float* dst = a.part_o + ro[row];
+                float* dst = a.part_o + pr * kDim;
                 const float4_t* rawp = reinterpret_cast<const float4_t*>(lds);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
@@ -944,7 +942,7 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
                     const int blk = (rbl * 17 + m) * 64 + 16 * glg + (row & 15);
                     float4_t acc = (float4_t)(-C);
 #pragma unroll
-                    for (int v = 0; v < kWaves; ++v) acc += rawp[v * 2 * 17 * 64 + blk] * f[v];
+                    for (int v = 0; v < kWaves; ++v) acc += rawp[v * (kWaveLds / 16) + blk] * f[v];
                     *reinterpret_cast<float4_t*>(dst + d) = acc;
                 }
             }
