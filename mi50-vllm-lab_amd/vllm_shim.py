@@ -14,7 +14,9 @@ few fields the routing reads.
 - forward_pth_dec (triton_attn.patch:116-174): the cache layout is checked once; the call falls
   back (returns False) without the softmax segment buffers, with more query tokens than segment
   rows, or with query / output strides the operator does not take. nsplit = min(splits,
-  segment count).
+  segment count); with a sliding window (every sequence sees at most window + qmax keys) it is
+  further capped at CUs / (kv heads x sequences), so that the partial kernel (one workgroup per
+  CU) runs in a single round.
 - forward_pth_fa (triton_attn.patch:176-262): the sequences with >= MIN_Q query tokens must form
   a suffix of the batch; the rows before it go to the decode operator when every prefix sequence
   has <= 4 (8 with DFlash) query tokens, else to the caller's Triton function. Each suffix
@@ -39,10 +41,36 @@ logger = logging.getLogger(__name__)
 PTH_FA_MIN_Q = int(os.environ.get("VLLM_GFX950_PTH_FA_MIN_Q", "64"))
 PTH_DEC_MAX_Q = int(os.environ.get("VLLM_GFX950_PTH_DEC_MAX_Q", "4"))
 PTH_DEC_SPLITS = int(os.environ.get("VLLM_GFX950_PTH_DEC_SPLITS", "64"))
+PTH_DEC_CUS = int(os.environ.get("VLLM_GFX950_PTH_DEC_CUS", "0"))  # 0: the device's CU count
 MAX_ROWS_PER_KV_HEAD = 48  # qmax * G the decode operator takes
 
 _dec_mod = None
 _fa_mod = None
+_cus = {}
+
+
+def cu_count(device) -> int:
+    """Compute units of `device` (cached; host-side query, no synchronisation). 256 for a CPU
+    device (tests) unless VLLM_GFX950_PTH_DEC_CUS is set."""
+    if PTH_DEC_CUS > 0:
+        return PTH_DEC_CUS
+    device = torch.device(device)
+    if device.type != "cuda":
+        return 256
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    if key not in _cus:
+        _cus[key] = torch.cuda.get_device_properties(key).multi_processor_count
+    return _cus[key]
+
+
+def decode_splits(nseg: int, window: int, num_kv_heads: int, num_seqs: int, device) -> int:
+    """Splits per sequence for the decode operator: min(VLLM_GFX950_PTH_DEC_SPLITS, nseg); with
+    a sliding window every sequence has about the same, bounded number of keys, so the grid
+    (splits x kv heads x sequences) is sized to one workgroup per CU."""
+    n = min(PTH_DEC_SPLITS, nseg)
+    if window > 0:
+        n = min(n, cu_count(device) // max(1, num_kv_heads * num_seqs))
+    return max(1, n)
 
 
 class _Operators:
@@ -153,7 +181,9 @@ class Gfx950Int8Attention:
         self.pth_dec.decode(query, key_cache, value_cache, k_scale_cache, v_scale_cache, block_table, seq_lens,
                             query_start_loc, output, self.scale, segm_o, meta.softmax_segm_max,
                             meta.softmax_segm_expsum, seq_lens.shape[0], max(1, max_q),
-                            min(PTH_DEC_SPLITS, segm_o.shape[2]), window=self.window, causal=True)
+                            decode_splits(segm_o.shape[2], self.window, self.num_kv_heads, seq_lens.shape[0],
+                                          query.device),
+                            window=self.window, causal=True)
         return True
 
     # -------------------------------------------------------------------------------------

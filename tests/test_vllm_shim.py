@@ -106,6 +106,18 @@ def test_decode_rows_route_to_decode_with_nsplit_cap(ops):
     assert (out == 1).all()
 
 
+@pytest.mark.parametrize("nseqs,nseg,want", [(4, 64, 16), (1, 64, 64), (2, 24, 24), (80, 64, 1)])
+def test_window_rows_fill_one_round_of_workgroups(ops, nseqs, nseg, want):
+    """With a sliding window the split count is capped at CUs / (kv heads x sequences) (256 CUs
+    on a CPU device): one round of partial workgroups."""
+    a = impl(sliding_window=(2047, -1))
+    q, out, kc = tensors(4 * nseqs)
+    m = meta([4] * nseqs, [3000 + 7 * i for i in range(nseqs)], nseg=nseg)
+    assert a.route(q, kc, kc, None, None, m, out, 4, 4 * nseqs, lambda *x: pytest.fail("fallback"))
+    assert ops.calls[-1][0] == "decode" and ops.calls[-1][4] == want
+    assert shim.decode_splits(nseg, -1, 4, nseqs, "cpu") == min(64, nseg)  # no window: no cap
+
+
 @pytest.mark.parametrize("why", ["no_segm", "too_many_tokens", "q_stride", "layout", "mid_q", "noncausal"])
 def test_decode_fallbacks(monkeypatch, why):
     f = FakeOps(layout_ok=why != "layout")
