@@ -155,6 +155,28 @@ def test_row_counts_and_masks(qlen, window, causal):
         assert emax <= 2e-3 and emean <= 2e-4, (ns, emax, emean)
 
 
+@pytest.mark.parametrize("qmax,window,causal", [(4, -1, True), (8, 512, False)])
+def test_large_batch_mixed_lengths(qmax, window, causal):
+    """130 sequences (the combine's token -> sequence lookup takes three 64-lane rounds), context
+    lengths 0-3,000 and 1..qmax query tokens each (some sequences without query tokens), so
+    splits range from empty to full and the grid runs several rounds of workgroups."""
+    g = np.random.default_rng(77 + qmax)
+    nseq = 130
+    ctxs = [int(x) for x in g.integers(0, 3000, nseq)]
+    qlens = [int(x) for x in g.integers(1, qmax + 1, nseq)]
+    for i in range(0, nseq, 29):
+        ctxs[i], qlens[i] = 0, 0  # padded graph slots
+    c = kvc.make_case(ctxs, qlens, num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=500 + qmax, window=window,
+                      causal=causal)
+    ref, written = oracle_of(c)
+    d = c.to("cuda")
+    for ns in (1, 6, 32):
+        say(f"large batch qmax={qmax} window={window} nsplit={ns}")
+        out = gpu_decode(d, ns)
+        emax, emean = errors(out, ref, written)
+        assert emax <= 2e-3 and emean <= 2e-4, (ns, emax, emean)  # (NaN would fail here too)
+
+
 @pytest.mark.parametrize("hq,hkv,qlens", [(8, 8, [4, 4]), (16, 8, [4, 3]), (12, 4, [4]), (20, 4, [3, 1]),
                                             (32, 4, [4]), (48, 1, [1])])
 def test_gqa_group_sizes(hq, hkv, qlens):
