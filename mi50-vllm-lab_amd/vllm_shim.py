@@ -14,9 +14,10 @@ few fields the routing reads.
 - forward_pth_dec (triton_attn.patch:116-174): the cache layout is checked once; the call falls
   back (returns False) without the softmax segment buffers, with more query tokens than segment
   rows, or with query / output strides the operator does not take. nsplit = min(splits,
-  segment count); with a sliding window (every sequence sees at most window + qmax keys) it is
-  further capped at CUs / (kv heads x sequences), so that the partial kernel (one workgroup per
-  CU) runs in a single round.
+  segment count). With host-side sequence lengths (vLLM's seq_lens_cpu) the count is chosen by a
+  makespan model of the partial kernel (one workgroup per CU; see decode_splits); without them a
+  sliding window (every sequence sees at most window + qmax keys) caps it at CUs / (kv heads x
+  sequences), so that the partial kernel runs in a single round.
 - forward_pth_fa (triton_attn.patch:176-262): the sequences with >= MIN_Q query tokens must form
   a suffix of the batch; the rows before it go to the decode operator when every prefix sequence
   has <= 4 (8 with DFlash) query tokens, else to the caller's Triton function. Each suffix
@@ -28,10 +29,12 @@ few fields the routing reads.
 from __future__ import annotations
 
 import logging
+import math
 import os
 from dataclasses import dataclass
 from typing import Any, Callable, Optional
 
+import numpy as np
 import torch
 
 from . import pth_dec as _pd
@@ -63,14 +66,46 @@ def cu_count(device) -> int:
     return _cus[key]
 
 
-def decode_splits(nseg: int, window: int, num_kv_heads: int, num_seqs: int, device) -> int:
-    """Splits per sequence for the decode operator: min(VLLM_GFX950_PTH_DEC_SPLITS, nseg); with
-    a sliding window every sequence has about the same, bounded number of keys, so the grid
-    (splits x kv heads x sequences) is sized to one workgroup per CU."""
-    n = min(PTH_DEC_SPLITS, nseg)
+# Makespan model of the decode partial kernel (grid splits x kv heads x sequences, one
+# workgroup per CU), fitted to MI355X measurements: a workgroup costs ~12 us of set-up and merge
+# plus ~3.3 us per 32-key tile of its busiest wave (4 waves share a split's tiles); a split
+# with no tiles ~2 us.
+SPLIT_FIXED_US, SPLIT_TILE_US, SPLIT_EMPTY_US = 12.0, 3.3, 2.0
+
+
+def decode_splits(nseg: int, window: int, num_kv_heads: int, num_seqs: int, device, seq_lens_host=None,
+                  max_q: int = 1) -> int:
+    """Splits per sequence for the decode operator, at most min(VLLM_GFX950_PTH_DEC_SPLITS, nseg).
+
+    With the host-side sequence lengths, the candidate (powers of two and the cap) with the
+    smallest modelled makespan max(total workgroup time / CUs, longest workgroup): few splits
+    for many sequences, many for one long sequence. Without them: a sliding window bounds every
+    sequence to about window + qmax keys, so the grid is sized to one workgroup per CU; otherwise
+    the cap (the reference's rule)."""
+    cap = max(1, min(PTH_DEC_SPLITS, nseg))
+    cus = cu_count(device)
+    if seq_lens_host is None:
+        if window > 0:
+            return max(1, min(cap, cus // max(1, num_kv_heads * num_seqs)))
+        return cap
+    lens = np.asarray(seq_lens_host, dtype=np.int64).reshape(-1)[:num_seqs]
     if window > 0:
-        n = min(n, cu_count(device) // max(1, num_kv_heads * num_seqs))
-    return max(1, n)
+        lens = np.minimum(lens, window + max_q)
+    tiles = (lens + 31) // 32 + (lens > 0)  # visible keys in 32-key tiles (+1: alignment)
+    live = tiles > 0
+    if not live.any():
+        return 1
+    cands = sorted({1 << k for k in range(int(math.log2(cap)) + 1)} | {cap})
+    best_s, best_t = cap, float("inf")
+    for s in cands:
+        per = np.maximum(-(-tiles // s), 1)              # tiles per split
+        n = np.where(live, -(-tiles // per), 0)         # splits holding tiles
+        t = SPLIT_FIXED_US + SPLIT_TILE_US * -(-per // 4)
+        total = num_kv_heads * float(np.sum(n * t + (s - n) * SPLIT_EMPTY_US))
+        span = max(total / cus, float(t[live].max()))
+        if span < best_t - 1e-9:
+            best_s, best_t = s, span
+    return best_s
 
 
 class _Operators:
@@ -132,6 +167,7 @@ class AttnMeta:
     softmax_segm_output: Optional[torch.Tensor] = None   # fp32 [T, Hq, nseg, 256]
     softmax_segm_max: Optional[torch.Tensor] = None      # fp32 [T, Hq, nseg]
     softmax_segm_expsum: Optional[torch.Tensor] = None   # fp32 [T, Hq, nseg]
+    seq_lens_cpu: Optional[Any] = None                   # the same lengths on the host, if known
     mm_prefix_range_tensor: Optional[torch.Tensor] = None
     rswa_prefix_lens: Optional[torch.Tensor] = None
 
@@ -165,7 +201,7 @@ class Gfx950Int8Attention:
 
     # -------------------------------------------------------------------------------------
     def forward_pth_dec(self, query, key_cache, value_cache, k_scale_cache, v_scale_cache, block_table, seq_lens,
-                        query_start_loc, output, max_q: int, meta: AttnMeta) -> bool:
+                        query_start_loc, output, max_q: int, meta: AttnMeta, seq_lens_host=None) -> bool:
         """Sequences with <= max_q query tokens through the decode operator. Launch only (no host
         sync, no allocation): safe in graphs. False: the caller runs its own path."""
         if self.layout_ok is None:
@@ -182,7 +218,7 @@ class Gfx950Int8Attention:
                             query_start_loc, output, self.scale, segm_o, meta.softmax_segm_max,
                             meta.softmax_segm_expsum, seq_lens.shape[0], max(1, max_q),
                             decode_splits(segm_o.shape[2], self.window, self.num_kv_heads, seq_lens.shape[0],
-                                          query.device),
+                                          query.device, seq_lens_host, max(1, max_q)),
                             window=self.window, causal=True)
         return True
 
@@ -205,7 +241,8 @@ class Gfx950Int8Attention:
             self.pth_dec is not None and max_q_prefix <= self.max_q
             and self.forward_pth_dec(query[:qsl[p]], key_cache, value_cache, k_scale_cache, v_scale_cache,
                                      meta.block_table[:p], meta.seq_lens[:p], meta.query_start_loc[:p + 1],
-                                     output[:qsl[p]], max_q_prefix, meta)):
+                                     output[:qsl[p]], max_q_prefix, meta,
+                                     None if meta.seq_lens_cpu is None else meta.seq_lens_cpu[:p])):
             triton_fallback(0, qsl[p], 0, p, max_q_prefix)
         for i in range(p, n):
             start, nq = qsl[i], qsl[i + 1] - qsl[i]
@@ -230,6 +267,6 @@ class Gfx950Int8Attention:
         if (self.pth_dec is not None and max_seqlen_q <= self.max_q and plain
                 and self.forward_pth_dec(query[:num_actual_tokens], key_cache, value_cache, k_scale_cache,
                                          v_scale_cache, meta.block_table, meta.seq_lens, meta.query_start_loc,
-                                         output[:num_actual_tokens], max_seqlen_q, meta)):
+                                         output[:num_actual_tokens], max_seqlen_q, meta, meta.seq_lens_cpu)):
             return True
         return False

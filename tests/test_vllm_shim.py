@@ -118,6 +118,37 @@ def test_window_rows_fill_one_round_of_workgroups(ops, nseqs, nseg, want):
     assert shim.decode_splits(nseg, -1, 4, nseqs, "cpu") == min(64, nseg)  # no window: no cap
 
 
+# (seq_lens incl. query tokens, qmax, window) -> the split count that measured fastest on
+# MI355X (µs per layer at 1 / 2 / 4 / 8 / 16 / 32 / 64 splits, 24 q / 4 kv heads, bs 16)
+MEASURED_BEST = [
+    ([8196] * 16, 4, -1, 4),                    # 171 / 98 / 72 / 83 / 103 / 141 / 202
+    ([4097] * 64, 1, -1, 1),                    # 124 / 124 / 133 / 159 / 203 / 271 / 411
+    ([120004] + [2052] * 7, 4, -1, 32),         # 1993 / 1011 / 519 / 273 / 151 / 91 / 119
+    ([61444], 4, -1, 64),                       # config 2 (MTP verify, 61k)
+    ([4097], 1, -1, 64),                        # config 1: 15.1 at 16, 13.4 at 32, 12.2 at 64
+    ([2056, 9224, 33800, 122888], 8, 2048, 16),  # config 3: 34.3 at 8, 32.6 at 16, 42.7 at 32
+]
+
+
+@pytest.mark.parametrize("lens,qmax,window,best", MEASURED_BEST)
+def test_split_model_picks_the_measured_best(lens, qmax, window, best):
+    assert shim.decode_splits(64, window, 4, len(lens), "cpu", lens, qmax) == best
+    assert shim.decode_splits(16, window, 4, len(lens), "cpu", lens, qmax) <= 16  # never above nseg
+
+
+def test_route_passes_host_lengths_to_the_split_model(ops):
+    a = impl()
+    nseq = 16
+    q, out, kc = tensors(4 * nseq)
+    m = meta([4] * nseq, [8196] * nseq)
+    m.seq_lens_cpu = [8196] * nseq
+    assert a.route(q, kc, kc, None, None, m, out, 4, 4 * nseq, lambda *x: pytest.fail("fallback"))
+    assert ops.calls[-1][0] == "decode" and ops.calls[-1][4] == 4
+    m2 = meta([4] * nseq, [8196] * nseq)  # no host lengths, no window: the reference's cap
+    assert a.route(q, kc, kc, None, None, m2, out, 4, 4 * nseq, lambda *x: None)
+    assert ops.calls[-1][4] == 64
+
+
 @pytest.mark.parametrize("why", ["no_segm", "too_many_tokens", "q_stride", "layout", "mid_q", "noncausal"])
 def test_decode_fallbacks(monkeypatch, why):
     f = FakeOps(layout_ok=why != "layout")
