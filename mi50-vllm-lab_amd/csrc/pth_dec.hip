@@ -17,8 +17,9 @@
 //   bytes [256, 512) of the rows (k_scale and V), one for bytes [504, 520) (the last V bytes and
 //   v_scale). With block_size a multiple of 16 a 16-key row block sits in one page, so each
 //   instruction is a scalar base (page, slot) plus a per-lane constant offset. Tile n + 1 is in
-//   flight while tile n is computed; tile n + 2 is issued into tile n's slot once tile n is
-//   done. The block-table slice of the split is staged in LDS once (as 64-bit row offsets), and
+//   flight while tile n is computed; tile n + 2 is issued into tile n's slot in two parts: its
+//   8 K copies as soon as tile n's operands are in registers (the queue space tile n has just
+//   freed takes them without a stall), the other 9 once tile n is done. The block-table slice of the split is staged in LDS once (as 64-bit row offsets), and
 //   with one or two row blocks Q is copied into LDS the same way, so the first tile is issued
 //   one memory round trip after the kernel starts.
 //
@@ -711,8 +712,9 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
 
     // rare path: raise the running max of the rows that need it, shift their relative scores and
     // rescale their state
-    // With three row blocks the rescale goes through LDS (4 KiB of scratch in the current tile's
-    // slot, whose operands are all in registers by now): the accumulators are then only ever
+    // With three row blocks the rescale goes through LDS (4 KiB of scratch in the V image of the
+    // current tile's slot: its operands are all in registers by now, and only the K image is
+    // already being refilled): the accumulators are then only ever
     // touched by MFMAs and by asm with AGPR operands, so the compiler keeps them in the AGPR
     // file (multiplying them in place made it spill ~250 registers, partly in the fast loop).
     // With fewer row blocks the registers suffice and the multiply in place is faster.
@@ -820,6 +822,25 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
             issue_tile<kFast>(a, tile_src<kFast, kLds>(a, pt, gbase, tile_of(n), tb, lo, hi, l), dl,
                               wslots + (unsigned)((n & 1) * kSlot), l);
         };
+        // The same copies in two parts (16-key row blocks): the 8 K blocks, then the 8 V blocks
+        // and the tail, from the addresses the first part looked up.
+        TileSrc nsrc;
+        auto issue_k = [&](int n) __attribute__((always_inline)) {
+            wait_lds();  // every LDS access to the slot being refilled has completed
+            nsrc = tile_src<kFast, kLds>(a, pt, gbase, tile_of(n), tb, lo, hi, l);
+            const unsigned slot = wslots + (unsigned)((n & 1) * kSlot);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                dma16_s(nsrc.base[i >> 2] + (int64_t)(4 * (i & 3)) * a.k_ss, dl.kvo, slot + kImgK + i * kBlk);
+        };
+        auto issue_v = [&](int n) __attribute__((always_inline)) {
+            const unsigned slot = wslots + (unsigned)((n & 1) * kSlot);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                dma16_s(nsrc.base[i >> 2] + (int64_t)(i & 3) * a.k_ss, dl.vvo, slot + kImgV + i * kBlk);
+            const int64_t delta = nsrc.base[1] - nsrc.base[0];
+            dma16_v<0>(nsrc.base[0] + (delta & -(int64_t)dl.tsel) + dl.toff, slot + kImgT);
+        };
         // The first two tiles (issued during the set-up when kEarly): all loads the compiler can
         // see (Q, block table) have been waited for by now, so no compiler-inserted wait will
         // include these copies.
@@ -844,20 +865,29 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
                 lds_u8* T = L + w * kWaveLds + (n & 1) * kSlot;
                 tile_cur = tile_of(n);
                 read_ops(T, ops);
+                if (kFast && n + 2 < nt) issue_k(n + 2);
                 const bool need = tile_scores(ops, sv, interior);
                 if (__builtin_amdgcn_ballot_w64(need) != 0) {
                     rare = true;
                     break;
                 }
                 tile_values(ops, sv, interior);
-                // Refill the slot with tile n + 2 once tile n is computed: the issue can stall
-                // while the memory queues are full, and stalling here overlaps the wait below.
-                if (n + 2 < nt) issue(n + 2);
+                if (n + 2 < nt) {
+                    if constexpr (kFast)
+                        issue_v(n + 2);
+                    else
+                        issue(n + 2);
+                }
             }
             if (!rare) break;
-            raise_max(sv, L + w * kWaveLds + (n & 1) * kSlot);
+            raise_max(sv, L + w * kWaveLds + (n & 1) * kSlot + kImgV);
             tile_values(ops, sv, interior);
-            if (n + 2 < nt) issue(n + 2);
+            if (n + 2 < nt) {
+                if constexpr (kFast)
+                    issue_v(n + 2);
+                else
+                    issue(n + 2);
+            }
             ++n;
         }
     };
