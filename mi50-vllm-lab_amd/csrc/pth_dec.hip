@@ -19,9 +19,10 @@
 //   instruction is a scalar base (page, slot) plus a per-lane constant offset. Tile n + 1 is in
 //   flight while tile n is computed; tile n + 2 is issued into tile n's slot in two parts: its
 //   8 K copies as soon as tile n's operands are in registers (the queue space tile n has just
-//   freed takes them without a stall), the other 9 once tile n is done. The block-table slice of the split is staged in LDS once (as 64-bit row offsets), and
-//   with one or two row blocks Q is copied into LDS the same way, so the first tile is issued
-//   one memory round trip after the kernel starts.
+//   freed takes them without a stall), the other 9 once tile n is done. The block-table slice
+//   of the split is staged in LDS once (as 64-bit row offsets), and with one or two row blocks
+//   Q is copied into LDS the same way, so the first tile (and the K copies of the second) is
+//   issued one memory round trip after the kernel starts.
 //
 // Per 32-key tile, per wave
 //   S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims of K (int8 widened to fp16
@@ -381,8 +382,9 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     constexpr int kLdsStats = kLdsWaves;                  // m, l: [wave][NRB][16]
     // kEarly: Q and the block-table slice are copied into LDS like the tiles, and each wave's
     // first tile is issued before anything is waited for (addressed with scalar block-table
-    // loads), so the copies start one memory round trip after the kernel does; the second tile
-    // follows the set-up (a copy issue stalls while the memory queues are full).
+    // loads), so the copies start one memory round trip after the kernel does; the second
+    // tile's K copies follow at once, its other copies after the set-up (a copy issue stalls
+    // while the memory queues are full).
     constexpr bool kEarly = kFast && NRB <= 2;
     constexpr int kLdsBt = kLdsStats + 2 * kWaves * NRB * 16 * 4;
     constexpr int kLdsRaw = kLdsBt + (kEarly ? kBtEarly : kBtCache) * 8;
@@ -549,10 +551,18 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
             for (int i = w; 64 * i < npages; i += kWaves)
                 dma4_v(bt_glob + min(pt.pfirst + 64 * i + l, plast), lds_base + (unsigned)(kLdsRaw + 256 * i));
         }
-        // (2) this wave's first tile; its second tile is issued once the set-up below is done
+        // (2) this wave's first tile
         if (nt > 0) issue_tile<kFast>(a, src0, dl, wslots, l);
+        // the K blocks of the second tile follow at once, its other copies after the set-up
+        if (nt > 1) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                dma16_s(src1.base[i >> 2] + (int64_t)(4 * (i & 3)) * a.k_ss, dl.kvo, wslots + kSlot + kImgK + i * kBlk);
+        }
         // (3) wait for (1) only
-        if (nt > 0)
+        if (nt > 1)
+            wait_vm<25>();
+        else if (nt > 0)
             wait_vm<17>();
         else
             wait_vm<0>();
@@ -579,7 +589,14 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
             }
         }
         __syncthreads();  // the block offsets are visible
-        if (nt > 1) issue_tile<kFast>(a, src1, dl, wslots + (unsigned)kSlot, l);
+        if (nt > 1) {
+            const unsigned slot = wslots + (unsigned)kSlot;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                dma16_s(src1.base[i >> 2] + (int64_t)(i & 3) * a.k_ss, dl.vvo, slot + kImgV + i * kBlk);
+            const int64_t delta = src1.base[1] - src1.base[0];
+            dma16_v<0>(src1.base[0] + (delta & -(int64_t)dl.tsel) + dl.toff, slot + kImgT);
+        }
     } else {
         const int pk_first = max(tb * kTile, lo), pk_last = min(te * kTile, hi) - 1;
         const int* bt_glob = a.block_table + (int64_t)b * a.bt_stride;
