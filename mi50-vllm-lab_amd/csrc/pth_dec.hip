@@ -17,9 +17,10 @@
 //   bytes [256, 512) of the rows (k_scale and V), one for bytes [504, 520) (the last V bytes and
 //   v_scale). With block_size a multiple of 16 a 16-key row block sits in one page, so each
 //   instruction is a scalar base (page, slot) plus a per-lane constant offset. Tile n + 1 is in
-//   flight while tile n is computed; tile n + 2 is issued into tile n's slot in two parts: its
-//   8 K copies as soon as tile n's operands are in registers (the queue space tile n has just
-//   freed takes them without a stall), the other 9 once tile n is done. The block-table slice
+//   flight while tile n is computed; tile n + 2 is issued into tile n's slot in parts: its 8 K
+//   copies as soon as tile n's operands are in registers (the queue space tile n has just freed
+//   takes them without a stall), the other 9 once tile n is done (in the first two iterations
+//   four of them already between the scores and the values). The block-table slice
 //   of the split is staged in LDS once (as 64-bit row offsets), and with one or two row blocks
 //   Q is copied into LDS the same way, so the first tile (and the K copies of the second) is
 //   issued one memory round trip after the kernel starts.
@@ -729,9 +730,9 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
 
     // rare path: raise the running max of the rows that need it, shift their relative scores and
     // rescale their state
-    // With three row blocks the rescale goes through LDS (4 KiB of scratch in the V image of the
-    // current tile's slot: its operands are all in registers by now, and only the K image is
-    // already being refilled): the accumulators are then only ever
+    // With three row blocks the rescale goes through LDS (4 KiB of scratch in V blocks 4..7 of
+    // the current tile's slot: its operands are all in registers by now, and only the K image and
+    // V blocks 0..3 can already be refilling): the accumulators are then only ever
     // touched by MFMAs and by asm with AGPR operands, so the compiler keeps them in the AGPR
     // file (multiplying them in place made it spill ~250 registers, partly in the fast loop).
     // With fewer row blocks the registers suffice and the multiply in place is faster.
@@ -850,10 +851,25 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
             for (int i = 0; i < 8; ++i)
                 dma16_s(nsrc.base[i >> 2] + (int64_t)(4 * (i & 3)) * a.k_ss, dl.kvo, slot + kImgK + i * kBlk);
         };
-        auto issue_v = [&](int n) __attribute__((always_inline)) {
+        // While the stream ramps up (the refills of its first kRampTiles tiles) the first four V
+        // blocks go between the scores and the values, the rest after the values.
+        constexpr int kRampTiles = 2;
+        auto ramp = [&](int n) { return n - 2 < kRampTiles; };  // refill n is issued by iteration n - 2
+        auto issue_v0 = [&](int n) __attribute__((always_inline)) {
             const unsigned slot = wslots + (unsigned)((n & 1) * kSlot);
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int i = 0; i < 4; ++i)
+                dma16_s(nsrc.base[i >> 2] + (int64_t)(i & 3) * a.k_ss, dl.vvo, slot + kImgV + i * kBlk);
+        };
+        auto issue_v = [&](int n) __attribute__((always_inline)) {
+            const unsigned slot = wslots + (unsigned)((n & 1) * kSlot);
+            if (!ramp(n)) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    dma16_s(nsrc.base[i >> 2] + (int64_t)(i & 3) * a.k_ss, dl.vvo, slot + kImgV + i * kBlk);
+            }
+#pragma unroll
+            for (int i = 4; i < 8; ++i)
                 dma16_s(nsrc.base[i >> 2] + (int64_t)(i & 3) * a.k_ss, dl.vvo, slot + kImgV + i * kBlk);
             const int64_t delta = nsrc.base[1] - nsrc.base[0];
             dma16_v<0>(nsrc.base[0] + (delta & -(int64_t)dl.tsel) + dl.toff, slot + kImgT);
@@ -884,6 +900,7 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
                 read_ops(T, ops);
                 if (kFast && n + 2 < nt) issue_k(n + 2);
                 const bool need = tile_scores(ops, sv, interior);
+                if (kFast && n + 2 < nt && ramp(n + 2)) issue_v0(n + 2);
                 if (__builtin_amdgcn_ballot_w64(need) != 0) {
                     rare = true;
                     break;
@@ -897,7 +914,7 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
                 }
             }
             if (!rare) break;
-            raise_max(sv, L + w * kWaveLds + (n & 1) * kSlot + kImgV);
+            raise_max(sv, L + w * kWaveLds + (n & 1) * kSlot + kImgV + 4 * kBlk);
             tile_values(ops, sv, interior);
             if (n + 2 < nt) {
                 if constexpr (kFast)
