@@ -21,9 +21,10 @@
 //   copies as soon as tile n's operands are in registers (the queue space tile n has just freed
 //   takes them without a stall), the other 9 once tile n is done (in the first two iterations
 //   four of them already between the scores and the values). The block-table slice
-//   of the split is staged in LDS once (as 64-bit row offsets), and with one or two row blocks
-//   Q is copied into LDS the same way, so the first tile (and the K copies of the second) is
-//   issued one memory round trip after the kernel starts.
+//   of the split is staged in LDS once (as 64-bit row offsets), and with block sizes that are
+//   multiples of 16 Q is copied into LDS the same way (48 rows: into the V images of the
+//   second slots of waves 0-2), so the first tile (and the K copies of the second) is issued one
+//   memory round trip after the kernel starts.
 //
 // Per 32-key tile, per wave
 //   S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims of K (int8 widened to fp16
@@ -44,8 +45,8 @@
 //
 // End of split: the 4 waves merge (m, l, O) through LDS and write one partial per row:
 //   part_o [T, Hq, nseg, 256] unnormalised, part_m [T, Hq, nseg] running max in log2 units,
-//   part_l the matching sum. With one or two row blocks each wave stores its accumulators
-//   straight from the AGPRs and the per-row factors are applied while summing. Splits with no
+//   part_l the matching sum. Each wave stores its accumulators straight from the AGPRs and the
+//   per-row factors are applied while summing. Splits with no
 //   tiles write m = -inf. The combine kernel merges the partials of each (token, head) with a
 //   log-sum-exp rescale.
 //
@@ -112,7 +113,8 @@ constexpr int kWaveLds = 2 * kSlot;                // LDS bytes per wave
 constexpr int kWaves = 4;                          // independent tile streams per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBtCache = 1024;                     // block-table entries of a split kept in LDS
-// With Q staged in LDS as well (one or two row blocks) the block-table slice is smaller:
+// With Q staged in LDS as well (block sizes that are multiples of 16) the block-table slice
+// is smaller:
 constexpr int kBtEarly = 384;                      // per-block row offsets (192 tiles per split)
 constexpr int kBtRaw = 384;                        // raw block-table entries of the split
 
@@ -381,17 +383,21 @@ template <int NRB, bool kFast>
 __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialParams a) {
     constexpr int kLdsWaves = kWaves * kWaveLds;
     constexpr int kLdsStats = kLdsWaves;                  // m, l: [wave][NRB][16]
-    // kEarly: Q and the block-table slice are copied into LDS like the tiles, and each wave's
+    // kEarly (block sizes that are multiples of 16): Q and the block-table slice are copied into
+    // LDS like the tiles, and each wave's
     // first tile is issued before anything is waited for (addressed with scalar block-table
     // loads), so the copies start one memory round trip after the kernel does; the second
     // tile's K copies follow at once, its other copies after the set-up (a copy issue stalls
     // while the memory queues are full).
-    constexpr bool kEarly = kFast && NRB <= 2;
+    constexpr bool kEarly = kFast;
     constexpr int kLdsBt = kLdsStats + 2 * kWaves * NRB * 16 * 4;
     constexpr int kLdsRaw = kLdsBt + (kEarly ? kBtEarly : kBtCache) * 8;
     constexpr int kLdsQ = kLdsRaw + (kEarly ? kBtRaw * 4 : 0);
     // the merge's table of V widening biases reuses the Q region (or follows the block table)
-    constexpr int kQBytes = kEarly ? 16 * NRB * 2 * kDim : 0;
+    // (three row blocks: Q is staged in the V images of slot 1 of waves 0..2 instead, 16 rows
+    // each; those slots receive their V copies only after Q is in registers)
+    constexpr bool kQInSlots = NRB >= 3;
+    constexpr int kQBytes = kEarly && !kQInSlots ? 16 * NRB * 2 * kDim : 0;
     constexpr int kMergeCBytes = kWaves * NRB * 16 * 4;
     constexpr int kLdsMergeC = kLdsQ;
     constexpr int kLdsBytes = kLdsQ + (kQBytes > kMergeCBytes ? kQBytes : kMergeCBytes);
@@ -545,7 +551,9 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
             const int r = min(2 * i + (l >> 5), R - 1);
             const int qi = r / G, qh = r - qi * G;
             const _Float16* qrow = a.q + (int64_t)(q0 + qi) * a.q_st + (int64_t)(g * G + qh) * kDim;
-            dma16_v<0>(reinterpret_cast<const int8_t*>(qrow) + 16 * (l & 31), lds_base + (unsigned)(kLdsQ + 1024 * i));
+            const int qdst = kQInSlots ? (2 * i / 16) * kWaveLds + kSlot + kImgV + (2 * i % 16) * (2 * kDim)
+                                       : kLdsQ + 1024 * i;
+            dma16_v<0>(reinterpret_cast<const int8_t*>(qrow) + 16 * (l & 31), lds_base + (unsigned)qdst);
         }
         if (pt.in_lds) {
             const int* bt_glob = a.block_table + (int64_t)b * a.bt_stride;
@@ -581,7 +589,8 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         }
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) {
-            const lds_u8* qrow = L + kLdsQ + (16 * rb + li) * (2 * kDim);
+            const lds_u8* qrow = kQInSlots ? L + rb * kWaveLds + kSlot + kImgV + li * (2 * kDim)
+                                           : L + kLdsQ + (16 * rb + li) * (2 * kDim);
 #pragma unroll
             for (int st = 0; st < 8; ++st) {
                 const int dim = 64 * (st >> 1) + 16 * lg + 8 * (st & 1);
