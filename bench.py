@@ -1,24 +1,37 @@
 #!/usr/bin/env python3
-"""Benchmark: MTP verify decode attention over a 61,444-token int8 paged KV cache on one MI355X.
+"""Benchmark of the int8-KV paged attention operators on one MI355X.
 
-Workload: 1 sequence, 4 causal query tokens, 24 q heads / 4 kv heads (GQA 6 -> 24 rows per kv
-head), head_dim 256, ctx 61,440 + 4, int8 per-token-head cache (K/V ~ N(0,1) quantised
-absmax/127), block_size 16, random page permutation, fp16 out. One step = one operator call
-(one attention layer: both kernels, all 24 heads).
+Headline (`value`): MTP verify decode, 1 sequence x 4 causal query tokens, 24 q heads / 4 kv
+heads (GQA 6 -> 24 rows per kv head), head_dim 256, ctx 61,440 + 4, int8 per-token-head cache
+(K/V ~ N(0,1) quantised absmax/127), block_size 16, random page permutation, fp16 out. One step =
+one operator call (one attention layer: both kernels, all 24 heads). Exactly `--steps` calls are
+captured in one HIP graph (each call reads the next of `--rotate` identical caches, so every layer
+reads its KV from HBM and not from the 256 MB Infinity Cache) and replayed once between device
+synchronisations, timed with HIP events on the stream the kernels run on; `--warmup` calls are
+replayed before, from a graph of their own.
 
-Every call reads a different one of `--rotate` identical caches, so each layer reads its KV from
-HBM as it would inside a model (a single 128 MB cache re-read back to back would be served
-partly by the 256 MB Infinity Cache). The calls are captured in a HIP graph and replayed; the
-timed region is bracketed by device synchronisation and measured with HIP events on the
-stream the kernels run on. The split-K partial kernel, which moves the KV bytes, is timed the
-same way on its own for the roofline. The CPU baseline is the float64 oracle on this host.
+`roofline`: the split-K partial kernel alone (the kernel that moves the KV bytes), a graph of a
+fixed 2,000 launches over the rotating caches, timed the same way: algorithmic bytes per launch
+/ average launch time against 8 TB/s. `traffic` and the MFMA counters come from the rocprofv3
+summaries committed under profiles/ for the same workload.
+
+`configs`: the other workloads, each with its own fixed repetition count:
+  1  single-token decode, 1 x 1 token, ctx 4,096 (6 rows per kv head)
+  3  DFlash2 drafter, 4 sequences (ctx 2,048 / 9,216 / 33,792 / 122,880) x 8 non-causal rows,
+     2,048-key sliding window, pages outside every window freed (NaN)
+  4  long context, 1 x 4 tokens, ctx 200,000, 1 % of the (token, kv head) rows x 50 before
+     quantisation: one call captured in a HIP graph and the graph replayed 1,000 times
+  5  chunked prefill, a 2,048-token causal chunk over 61,440 cached tokens (63,488 keys)
+Decode configs report µs per layer, algorithmic GB/s and the fraction of 8 TB/s; the prefill
+reports ms per chunk and TFLOP/s against the 2.5 PFLOP/s dense fp16 MFMA peak. The split count
+of each decode config is the one the vLLM shim picks (vllm_shim.decode_splits with the host-side
+lengths); config 2 uses the reference's 64.
+
+CPU baselines: the float64 oracle (numpy + BLAS on every host core) on the same layer for
+configs 1, 2 and 4 (median of 5 runs after one warm-up), and on a sample of query rows for
+config 5.
 
 Prints one JSON line.
-
-`--prefill` instead measures the chunked-prefill operator (forward_pth interface) on a 2048-token
-causal chunk over 61,440 cached tokens (63,488 keys), 24 q / 4 kv heads, block_size 16: one step
-is one operator call; the line reports TFLOP/s against the fp16 MFMA peak, and the CPU baseline is
-the float64 oracle on a sample of query rows.
 """
 import argparse
 import json
@@ -32,14 +45,16 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG_DIR = os.path.join(ROOT, "mi50-vllm-lab_amd")
 sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 METRIC = "µs/layer + achieved KV GB/s (% of HBM peak), MTP 24-row decode at 61k ctx"
 HBM_PEAK_GBS = 8000.0
 MFMA_FP16_PEAK_TFLOPS = 2500.0
-PREFILL_METRIC = "TFLOP/s (MFMA fp16 peak 2.5 PF/s), 2048-token int8-KV chunked prefill over 63,488 keys"
 NSEG = 128
+ROOF_LAUNCHES = 2000
 CALIB_BYTES = 256 << 20
 CALIB_COPIES = 8
+PROFILES = os.path.join(ROOT, "profiles")
 
 
 def _pmc_dispatches(run_dir, counter):
@@ -63,7 +78,7 @@ def _pmc_dispatches(run_dir, counter):
 
 
 def summarize_traffic(args):
-    """HBM bytes per pd_partial_kernel launch from FETCH_SIZE and WRITE_SIZE runs of --profile-only.
+    """HBM bytes per partial-kernel launch from FETCH_SIZE and WRITE_SIZE runs of --profile-only.
 
     Both counters are read in KiB per dispatch. Each is scaled by what it reads for the calibration
     copy (CALIB_BYTES read and CALIB_BYTES written per launch, the last CALIB_COPIES dispatches)."""
@@ -71,7 +86,7 @@ def summarize_traffic(args):
     for counter, run_dir in (("FETCH_SIZE", args.traffic_summary[0]), ("WRITE_SIZE", args.traffic_summary[1])):
         d = _pmc_dispatches(run_dir, counter)
         order = sorted(d)
-        part = [d[k][1] for k in order if "pd_partial_kernel" in d[k][0]]
+        part = [d[k][1] for k in order if "partial" in d[k][0]]
         other = [d[k][1] for k in order if not d[k][0].startswith("pd_")]
         calib = other[-CALIB_COPIES:]
         if not part or len(calib) < CALIB_COPIES:
@@ -83,7 +98,7 @@ def summarize_traffic(args):
         res[counter] = {"partial_kib_median": p_kib, "calib_copy_kib_median": c_kib, "calib_factor": factor,
                         "partial_bytes": p_kib * 1024.0 * factor, "dispatches": len(part)}
     total = res["FETCH_SIZE"]["partial_bytes"] + res["WRITE_SIZE"]["partial_bytes"]
-    summary = {"kernel": "pd_partial_kernel", "workload": "MTP verify 4 x 24/4 heads, ctx 61440+4, bs 16",
+    summary = {"kernel": "decode partial kernel", "workload": "MTP verify 4 x 24/4 heads, ctx 61440+4, bs 16",
                "nsplit": args.nsplit, "hbm_bytes_per_launch": round(total), "counters": res,
                "calibration": f"{CALIB_COPIES} copies of {CALIB_BYTES} bytes (read + write) after the partial "
                               f"launches; factor = known bytes / counter bytes"}
@@ -116,12 +131,47 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def build_workload(kvc, ctx, qlen, seed):
-    return kvc.make_case([ctx], [qlen], num_q_heads=24, num_kv_heads=4, block_size=16, seed=seed)
+def decode_case(wl, n):
+    """The decode workloads (seed 1000 + config number)."""
+    s = 1000 + n
+    if n == 1:
+        return wl.make_case([4096], [1], num_q_heads=24, num_kv_heads=4, block_size=16, seed=s)
+    if n == 2:
+        return wl.make_case([61440], [4], num_q_heads=24, num_kv_heads=4, block_size=16, seed=s)
+    if n == 3:
+        return wl.make_case([2048, 9216, 33792, 122880], [8, 8, 8, 8], num_q_heads=24, num_kv_heads=4,
+                            block_size=16, seed=s, causal=False, window=2048, poison=True)
+    if n == 4:
+        return wl.make_case([200000], [4], num_q_heads=24, num_kv_heads=4, block_size=16, seed=s,
+                            outlier_frac=0.01, outlier_mult=50.0)
+    raise ValueError(n)
 
 
-def time_graph(torch, graph, replays, stream):
-    """Average ms per replay of `graph`, HIP events on `stream`, synchronised on both sides."""
+DESCRIPTIONS = {
+    1: "single-token decode: 1 seq x 1 query token, 24 q / 4 kv heads, ctx 4096+1, bs 16",
+    2: "MTP verify decode: 1 seq x 4 query tokens, 24 q / 4 kv heads, head_dim 256, ctx 61440+4 int8 "
+       "per-token-head paged KV, block_size 16",
+    3: "DFlash2 drafter decode: 4 seqs (ctx 2048/9216/33792/122880) x 8 non-causal query tokens, 2048-key "
+       "sliding window, freed pages NaN, 24 q / 4 kv heads, bs 16",
+    4: "long-context decode: 1 seq x 4 query tokens, ctx 200000+4, 1% outlier rows x50, bs 16, one call "
+       "captured in a HIP graph and replayed 1000x",
+    5: "chunked prefill: 1 seq, 2048-token causal chunk over 61440 cached tokens (63488 keys), 24 q / 4 kv "
+       "heads, head_dim 256, int8 per-token-head paged KV, bs 16",
+}
+
+
+def graph_of(torch, stream, calls):
+    """A HIP graph holding `calls` (a list of zero-argument launch functions), captured on `stream`."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for fn in calls:
+            fn()
+    return g
+
+
+def time_replays(torch, graph, replays, stream):
+    """ms for `replays` back-to-back replays of `graph`: HIP events on `stream`, device
+    synchronisation on both sides."""
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -130,32 +180,101 @@ def time_graph(torch, graph, replays, stream):
         graph.replay()
     end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / replays
+    return start.elapsed_time(end)
+
+
+class DecodeBench:
+    """A decode workload on the device: rotating cache copies, output and segment buffers, and the
+    operator call / partial-kernel call on a given copy."""
+
+    def __init__(self, torch, wl, pd, dev, case, copies, nsplit):
+        self.case = case
+        self.d = d = case.to(dev)
+        self.caches = [d.cache] + [wl.clone_cache(d.cache) for _ in range(copies - 1)]
+        T, HQ = d.num_tokens, d.num_q_heads
+        self.out = torch.empty((T, HQ, 256), dtype=torch.float16, device=dev)
+        self.po, self.pm, self.pl = wl.partial_buffers(T, HQ, NSEG, dev)
+        self.nsplit = nsplit
+        self.pd = pd
+        self.alg_bytes = wl.algorithmic_bytes(case)
+        # the partial pass writes no output rows
+        self.partial_bytes = self.alg_bytes - 2 * T * HQ * 256
+        self.flops = wl.algorithmic_flops(case)
+
+    def op(self, i):
+        d, c = self.d, self.caches[i % len(self.caches)]
+        return lambda: self.pd.decode(d.q, c.key_cache, c.value_cache, c.k_scale, c.v_scale, d.block_table,
+                                      d.seq_lens, d.query_start_loc, self.out, d.scale, self.po, self.pm, self.pl,
+                                      d.num_seqs, d.qmax, self.nsplit, d.window, d.causal)
+
+    def partial(self, i):
+        d, c = self.d, self.caches[i % len(self.caches)]
+
+        def run():
+            rc = self.pd.launch_partial(d.q, c.key_cache, d.block_table, d.seq_lens, d.query_start_loc, self.po,
+                                        self.pm, self.pl, num_seqs=d.num_seqs, heads_q=d.num_q_heads,
+                                        heads_kv=c.num_kv_heads, block_size=c.block_size, scale=d.scale,
+                                        qmax=d.qmax, nsplit=self.nsplit, window=d.window, causal=d.causal)
+            if rc != 0:
+                raise RuntimeError(f"pth_dec_launch_partial failed: {rc}")
+        return run
+
+
+def cpu_decode_baseline(orc, case, runs, what):
+    """Median seconds of the float64 oracle on the whole layer (after one warm-up)."""
+    import numpy as np
+
+    def once():
+        orc.paged_decode(case.q, case.cache.key_cache, case.cache.value_cache, case.cache.k_scale,
+                         case.cache.v_scale, case.block_table, case.seq_lens, case.query_start_loc, case.num_seqs,
+                         case.scale, case.window, case.causal)
+
+    once()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return med, (f"float64 numpy oracle (oracle/attention.py) on the full {what} layer (all 24 heads), median of "
+                 f"{runs} runs after 1 warm-up, numpy/BLAS threads on {os.cpu_count()} cores ({cpu_model()})")
+
+
+def decode_line(us, db):
+    gbs = db.alg_bytes / (us * 1e-6) / 1e9
+    return {"us_per_layer": round(us, 3), "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": db.alg_bytes, "nsplit": db.nsplit,
+            "tflops": round(db.flops / (us * 1e-6) / 1e12, 2)}
+
+
+def committed_profile(name):
+    p = os.path.join(PROFILES, name)
+    if not os.path.exists(p):
+        return None
+    try:
+        with open(p) as f:
+            return json.load(f)
+    except Exception:
+        return None
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=4000, help="timed operator calls")
-    ap.add_argument("--warmup", type=int, default=200, help="untimed operator calls")
-    ap.add_argument("--nsplit", type=int, default=64)
-    ap.add_argument("--rotate", type=int, default=8, help="distinct KV caches cycled through")
-    ap.add_argument("--ctx", type=int, default=61440)
-    ap.add_argument("--qlen", type=int, default=4)
+    ap.add_argument("--steps", type=int, default=2000, help="timed operator calls (config 2)")
+    ap.add_argument("--warmup", type=int, default=200, help="untimed operator calls before them")
+    ap.add_argument("--nsplit", type=int, default=64, help="config 2 split count")
+    ap.add_argument("--rotate", type=int, default=8, help="distinct config-2 KV caches cycled through")
+    ap.add_argument("--configs", default="1,3,4,5", help="other configs to measure ('' for none)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=5)
     ap.add_argument("--profile-only", action="store_true",
-                    help="replay the partial kernel only, then a plain copy of known size that calibrates the "
-                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters (for counter runs)")
-    ap.add_argument("--hot", action="store_true",
-                    help="also time every call on the same (Infinity-Cache resident) cache; reported beside")
+                    help="replay the config-2 partial kernel only (--steps launches), then plain copies of known "
+                         "size that calibrate the rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="no GPU work: turn two rocprofv3 --pmc runs of --profile-only (FETCH_SIZE, WRITE_SIZE) "
                          "into HBM bytes per partial launch, written to --traffic-out")
-    ap.add_argument("--traffic-out", default=os.path.join(ROOT, "profiles", "pd_partial_mtp61k_traffic.json"))
-    ap.add_argument("--prefill", action="store_true", help="measure the chunked-prefill operator instead")
-    ap.add_argument("--chunk", type=int, default=2048, help="--prefill: query tokens per chunk")
-    ap.add_argument("--cpu-rows", type=int, default=24, help="--prefill: query rows in the CPU baseline sample")
+    ap.add_argument("--traffic-out", default=os.path.join(PROFILES, "pd_partial_mtp61k_traffic.json"))
     args = ap.parse_args()
 
     if args.traffic_summary:
@@ -163,151 +282,136 @@ def main():
         return
 
     if args.gpus != 1:
-        print(json.dumps({"error": f"--gpus {args.gpus}: this benchmark measures one GPU; the operator is "
-                                   "single-GPU (multi-GPU runs shard by kv head and are not part of this build)"}))
+        print(json.dumps({"error": f"--gpus {args.gpus}: this benchmark measures one GPU; the operators are "
+                                   "single-GPU (a multi-GPU deployment shards them by kv head) and no multi-GPU "
+                                   "run is part of this build"}))
         sys.exit(2)
 
     import torch
 
+    import workload as wl
+
     pkg = load_package()
-    kvc, pd = pkg.kvcache, pkg.pth_dec
+    pd = pkg.pth_dec
     pd.load_library()
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-
-    if args.prefill:
-        bench_prefill(args, torch, kvc, pd, dev)
-        return
-
-    seed = 1002
-    case = build_workload(kvc, args.ctx, args.qlen, seed)
-    alg_bytes = kvc.algorithmic_bytes(case)
-    kv_bytes = kvc.visible_kv_bytes(case)
-    flops = kvc.algorithmic_flops(case)
-    partial_bytes = alg_bytes - 2 * case.num_tokens * case.num_q_heads * 256  # the partial pass writes no out
-
-    d = case.to(dev)
-    caches = [d.cache] + [kvc.clone_cache(d.cache) for _ in range(args.rotate - 1)]
-    T, HQ, HKV = d.num_tokens, d.num_q_heads, d.cache.num_kv_heads
-    out = torch.empty((T, HQ, 256), dtype=torch.float16, device=dev)
-    po, pm, pl = kvc.partial_buffers(T, HQ, NSEG, dev)
-    qmax = d.qmax
-
-    def op(cache):
-        pd.decode(d.q, cache.key_cache, cache.value_cache, cache.k_scale, cache.v_scale, d.block_table,
-                  d.seq_lens, d.query_start_loc, out, d.scale, po, pm, pl, 1, qmax, args.nsplit)
-
-    def partial(cache):
-        rc = pd.launch_partial(d.q, cache.key_cache, d.block_table, d.seq_lens, d.query_start_loc, po, pm, pl,
-                               num_seqs=1, heads_q=HQ, heads_kv=HKV, block_size=16, scale=d.scale, qmax=qmax,
-                               nsplit=args.nsplit)
-        if rc != 0:
-            raise RuntimeError(f"pth_dec_launch_partial failed: {rc}")
-
     stream = torch.cuda.Stream()
-    # eager warm-up on the side stream, then capture one rotation of calls per graph
-    with torch.cuda.stream(stream):
-        for c in caches:
-            op(c)
-    torch.cuda.synchronize()
-    g_op, g_part = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g_op, stream=stream):
-        for c in caches:
-            op(c)
-    with torch.cuda.graph(g_part, stream=stream):
-        for c in caches:
-            partial(c)
+
+    case2 = decode_case(wl, 2)
+    b2 = DecodeBench(torch, wl, pd, dev, case2, args.rotate, args.nsplit)
+    R = len(b2.caches)
+    with torch.cuda.stream(stream):  # eager warm-up of both paths on the side stream
+        for i in range(R):
+            b2.op(i)()
+            b2.partial(i)()
     torch.cuda.synchronize()
 
-    R = len(caches)
     if args.profile_only:
-        for _ in range(max(1, args.steps // R)):
-            g_part.replay()
+        g = graph_of(torch, stream, [b2.partial(i) for i in range(args.steps)])
+        with torch.cuda.stream(stream):
+            g.replay()
         torch.cuda.synchronize()
-        # calibration: CALIB_COPIES plain device copies of CALIB_BYTES each, launched last
         src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
         for _ in range(CALIB_COPIES):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"profile_only": True, "partial_launches": R * max(1, args.steps // R),
-                          "nsplit": args.nsplit, "calib_copies": CALIB_COPIES, "calib_bytes": CALIB_BYTES}))
+        print(json.dumps({"profile_only": True, "partial_launches": args.steps, "nsplit": args.nsplit,
+                          "calib_copies": CALIB_COPIES, "calib_bytes": CALIB_BYTES}))
         return
 
-    warm_reps = max(1, math.ceil(args.warmup / R))
-    reps = max(1, math.ceil(args.steps / R))
-    steps = reps * R
+    steps, warmup = max(1, args.steps), max(0, args.warmup)
+    g_steps = graph_of(torch, stream, [b2.op(i) for i in range(steps)])
+    g_warm = graph_of(torch, stream, [b2.op(i) for i in range(warmup)]) if warmup else None
+    g_roof = graph_of(torch, stream, [b2.partial(i) for i in range(ROOF_LAUNCHES)])
+    torch.cuda.synchronize()
     with torch.cuda.stream(stream):
-        for _ in range(warm_reps):
-            g_op.replay()
-        ms_rot = time_graph(torch, g_op, reps, stream) / R           # per layer, cold caches
-        for _ in range(warm_reps):
-            g_part.replay()
-        part_ms = time_graph(torch, g_part, reps, stream) / R         # partial kernel per launch
-    ms_hot = None
-    if args.hot:
-        # same cache every call (Infinity-Cache resident): reported beside, never as `value`
-        g_hot = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g_hot, stream=stream):
-            for _ in range(R):
-                op(caches[0])
+        if g_warm is not None:
+            g_warm.replay()
+        ms_total = time_replays(torch, g_steps, 1, stream)
+        g_roof.replay()  # warm
+        roof_ms = time_replays(torch, g_roof, 1, stream) / ROOF_LAUNCHES
+    ms_step = ms_total / steps
+    us_layer = ms_step * 1e3
+    gbs = b2.alg_bytes / (ms_step * 1e-3) / 1e9
+    part_gbs = b2.partial_bytes / (roof_ms * 1e-3) / 1e9
+
+    traffic_j = committed_profile("pd_partial_mtp61k_traffic.json")
+    traffic = traffic_j.get("hbm_bytes_per_launch") if traffic_j and traffic_j.get("nsplit") == args.nsplit else None
+    counters = committed_profile("pd_partial_mtp61k_counters.json")
+
+    want = [int(x) for x in args.configs.split(",") if x.strip()]
+    configs = {}
+    shim = pkg.vllm_shim
+    for n in (1, 3, 4):
+        if n not in want:
+            continue
+        c = decode_case(wl, n)
+        ns = shim.decode_splits(NSEG, c.window, 4, c.num_seqs, dev, c.seq_lens.tolist(), c.qmax)
+        copies = {1: 32, 3: 2, 4: 1}[n]
+        db = DecodeBench(torch, wl, pd, dev, c, copies, ns)
         with torch.cuda.stream(stream):
-            for _ in range(warm_reps):
-                g_hot.replay()
-            ms_hot = time_graph(torch, g_hot, reps, stream) / R
-
-    us_layer = ms_rot * 1e3
-    gbs = alg_bytes / (ms_rot * 1e-3) / 1e9
-    part_gbs = partial_bytes / (part_ms * 1e-3) / 1e9
-
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "pd_partial_mtp61k_traffic.json")
-    if os.path.exists(tpath):
-        try:
-            with open(tpath) as f:
-                t = json.load(f)
-            if t.get("nsplit") == args.nsplit:
-                traffic = t.get("hbm_bytes_per_launch")
-        except Exception:
-            traffic = None
+            for i in range(copies):
+                db.op(i)()
+        torch.cuda.synchronize()
+        if n == 4:
+            g = graph_of(torch, stream, [db.op(0)])
+            reps, per = 1000, 1
+        else:
+            g = graph_of(torch, stream, [db.op(i) for i in range(copies)])
+            reps, per = (30 if n == 1 else 250), copies
+        with torch.cuda.stream(stream):
+            for _ in range(max(1, reps // 10)):
+                g.replay()
+            ms = time_replays(torch, g, reps, stream)
+        us = ms * 1e3 / (reps * per)
+        line = decode_line(us, db)
+        line["workload"] = DESCRIPTIONS[n]
+        line["timed"] = f"{reps} replays of a {per}-call graph" + ("" if n == 4 else f" over {copies} cache copies")
+        configs[str(n)] = line
+        del db, g
+        torch.cuda.empty_cache()
+    if 5 in want:
+        configs["5"] = bench_prefill(torch, wl, pd, dev, stream)
 
     cpu = None
     if not args.no_cpu_baseline:
-        import numpy as np
-
         from oracle import attention as orc
 
-        def cpu_once():
-            orc.paged_decode(case.q, case.cache.key_cache, case.cache.value_cache, case.cache.k_scale,
-                             case.cache.v_scale, case.block_table, case.seq_lens, case.query_start_loc, 1,
-                             case.scale, -1, True)
+        med, sample = cpu_decode_baseline(orc, case2, args.cpu_runs, "config-2")
+        cpu = {"value": round(b2.alg_bytes / med / 1e9, 4), "unit": "GB/s", "cores": os.cpu_count(), "kind": "port",
+               "us_per_layer": round(med * 1e6, 1), "sample": sample, "gpu_speedup": round(med * 1e6 / us_layer, 1)}
+        for n in (1, 4):
+            if str(n) in configs:
+                c = decode_case(wl, n)
+                m, s = cpu_decode_baseline(orc, c, args.cpu_runs, f"config-{n}")
+                configs[str(n)]["cpu_baseline"] = {
+                    "us_per_layer": round(m * 1e6, 1), "GB_s": round(wl.algorithmic_bytes(c) / m / 1e9, 4),
+                    "cores": os.cpu_count(), "kind": "port", "sample": s,
+                    "gpu_speedup": round(m * 1e6 / configs[str(n)]["us_per_layer"], 1)}
+        if "5" in configs:
+            configs["5"]["cpu_baseline"] = cpu_prefill_baseline(torch, wl, orc)
 
-        cpu_once()  # warm-up
-        times = []
-        for _ in range(args.cpu_runs):
-            t0 = time.perf_counter()
-            cpu_once()
-            times.append(time.perf_counter() - t0)
-        med = float(np.median(times))
-        cpu = {"value": alg_bytes / med / 1e9, "unit": "GB/s", "cores": os.cpu_count(), "kind": "port",
-               "us_per_layer": med * 1e6,
-               "sample": f"float64 numpy oracle (oracle/attention.py), the full config-2 layer, median of "
-                         f"{args.cpu_runs} runs after 1 warm-up, numpy/BLAS threads on {os.cpu_count()} cores "
-                         f"({cpu_model()})",
-               "gpu_speedup": med * 1e6 / us_layer}
-
+    roofline = {"bound": "hbm", "achieved": round(part_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(part_gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": pd.partial_kernel_name(24, 16),
+                "avg_launch_us": round(roof_ms * 1e3, 3), "launches": ROOF_LAUNCHES,
+                "bytes_per_launch": b2.partial_bytes}
+    if counters:
+        roofline["mfma_busy"] = counters.get("mfma_busy")
+        roofline["counters_from"] = "profiles/pd_partial_mtp61k_counters.json"
     line = {
         "metric": METRIC,
         "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": warm_reps * R,
-        "ms_per_step": round(ms_rot, 6),
+        "warmup": warmup,
+        "ms_per_step": round(ms_step, 6),
         "us_per_layer": round(us_layer, 3),
         "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
         "higher_is_better": True,
@@ -315,107 +419,75 @@ def main():
         "vs_baseline": None,
         "dtype": "int8 KV / fp16 MFMA / fp32 softmax",
         "data": "synthetic (seeded N(0,1) K/V quantised absmax/127, random page permutation)",
-        "config": {"workload": f"MTP verify decode: 1 seq x {args.qlen} query tokens, 24 q / 4 kv heads, "
-                               f"head_dim 256, ctx {args.ctx}+{args.qlen} int8 per-token-head paged KV, "
-                               f"block_size 16",
-                   "nsplit": args.nsplit, "rotating_caches": R, "algorithmic_bytes": alg_bytes,
-                   "kv_bytes": kv_bytes, "flops": flops},
-        "roofline": {"bound": "hbm", "achieved": round(part_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(part_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "pd_partial_kernel", "avg_launch_us": round(part_ms * 1e3, 3),
-                     "bytes_per_launch": partial_bytes},
-        "hot_cache_us_per_layer": None if ms_hot is None else round(ms_hot * 1e3, 3),
-        "tflops": round(flops / (ms_rot * 1e-3) / 1e12, 2),
+        "config": {"workload": DESCRIPTIONS[2], "nsplit": args.nsplit, "rotating_caches": R,
+                   "algorithmic_bytes": b2.alg_bytes, "kv_bytes": wl.visible_kv_bytes(case2), "flops": b2.flops,
+                   "timed": f"one replay of a {steps}-call graph"},
+        "roofline": roofline,
+        "tflops": round(b2.flops / (ms_step * 1e-3) / 1e12, 2),
         "cpu_baseline": cpu,
+        "configs": configs,
     }
     print(json.dumps(line))
 
 
-def bench_prefill(args, torch, kvc, pd, dev):
-    """One JSON line for the chunked-prefill operator (see the module docstring)."""
-    ctx, sq = args.ctx, args.chunk
-    steps = max(1, min(args.steps, 200)) if args.steps != 4000 else 20
-    warm = max(1, min(args.warmup, 20)) if args.warmup != 200 else 3
-    case = kvc.make_case([ctx], [sq], num_q_heads=24, num_kv_heads=4, block_size=16, seed=1005)
-    flops = kvc.prefill_flops([ctx + sq], [ctx], sq, 24)
+PREFILL_CTX, PREFILL_CHUNK = 61440, 2048
+
+
+def bench_prefill(torch, wl, pd, dev, stream, reps=20):
+    """Config 5: ms per chunk and TFLOP/s of the chunked-prefill operator."""
+    ctx, sq = PREFILL_CTX, PREFILL_CHUNK
+    case = wl.make_case([ctx], [sq], num_q_heads=24, num_kv_heads=4, block_size=16, seed=1005)
+    flops = wl.prefill_flops([ctx + sq], [ctx], sq, 24)
     d = case.to(dev)
-    caches = [d.cache, kvc.clone_cache(d.cache)]
-    q = kvc.prefill_query(d)
+    caches = [d.cache, wl.clone_cache(d.cache)]
+    q = wl.prefill_query(d)
     qa = torch.tensor([ctx], dtype=torch.int32, device=dev)
     out = torch.empty((1, sq, 24, 256), dtype=torch.float32, device=dev)
 
     def op(c):
-        pd.forward_pth(q, c.key_cache, c.value_cache, d.block_table, d.seq_lens, d.scale, qa, out=out)
+        return lambda: pd.forward_pth(q, c.key_cache, c.value_cache, d.block_table, d.seq_lens, d.scale, qa, out=out)
 
-    stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
         for c in caches:
-            op(c)
+            op(c)()
     torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=stream):
-        for c in caches:
-            op(c)
-    torch.cuda.synchronize()
-    R = len(caches)
-    reps = max(1, math.ceil(steps / R))
+    g = graph_of(torch, stream, [op(c) for c in caches])
     with torch.cuda.stream(stream):
-        for _ in range(max(1, math.ceil(warm / R))):
-            g.replay()
-        ms = time_graph(torch, g, reps, stream) / R
+        g.replay()
+        ms = time_replays(torch, g, reps // 2, stream) / reps
     tflops = flops / (ms * 1e-3) / 1e12
+    return {"workload": DESCRIPTIONS[5], "ms_per_chunk": round(ms, 4), "TFLOP_s": round(tflops, 1),
+            "frac": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4), "flops": flops, "peak": MFMA_FP16_PEAK_TFLOPS,
+            "bound": "mfma", "timed": f"{reps // 2} replays of a 2-call graph over 2 cache copies"}
 
-    cpu = None
-    if not args.no_cpu_baseline:
-        import numpy as np
 
-        from oracle import attention as orc
+def cpu_prefill_baseline(torch, wl, orc, nrows=24):
+    import numpy as np
 
-        rows = np.linspace(0, sq - 1, args.cpu_rows).astype(int).tolist()
-        qcpu = kvc.prefill_query(case)
-        qa_cpu = torch.tensor([ctx], dtype=torch.int32)
+    ctx, sq = PREFILL_CTX, PREFILL_CHUNK
+    case = wl.make_case([ctx], [sq], num_q_heads=24, num_kv_heads=4, block_size=16, seed=1005)
+    flops = wl.prefill_flops([ctx + sq], [ctx], sq, 24)
+    rows = np.linspace(0, sq - 1, nrows).astype(int).tolist()
+    qcpu = wl.prefill_query(case)
+    qa_cpu = torch.tensor([ctx], dtype=torch.int32)
 
-        def cpu_once():
-            orc.paged_prefill(qcpu, case.cache.key_cache, case.cache.value_cache, case.cache.k_scale,
-                              case.cache.v_scale, case.block_table, case.seq_lens, case.scale, qa_cpu, rows)
+    def once():
+        orc.paged_prefill(qcpu, case.cache.key_cache, case.cache.value_cache, case.cache.k_scale, case.cache.v_scale,
+                          case.block_table, case.seq_lens, case.scale, qa_cpu, rows)
 
-        cpu_once()
-        times = []
-        for _ in range(3):
-            t0 = time.perf_counter()
-            cpu_once()
-            times.append(time.perf_counter() - t0)
-        med = float(np.median(times))
-        sample_flops = 4 * 256 * 24 * sum(min(ctx + sq, ctx + r + 1) for r in rows)
-        cpu = {"value": round(sample_flops / med / 1e12, 6), "unit": "TFLOP/s", "cores": os.cpu_count(),
-               "kind": "port",
-               "sample": f"float64 numpy oracle (oracle/attention.py paged_prefill) on {len(rows)} of the {sq} "
-                         f"query rows (all 24 heads, full visible context each), median of 3 runs after 1 "
-                         f"warm-up, BLAS threads on {os.cpu_count()} cores ({cpu_model()})",
-               "est_ms_full_chunk": round(flops / (sample_flops / med) * 1e3, 1)}
-
-    line = {
-        "metric": PREFILL_METRIC,
-        "value": round(tflops, 1),
-        "unit": "TFLOP/s",
-        "n_gpus": 1,
-        "steps": reps * R,
-        "warmup": max(1, math.ceil(warm / R)) * R,
-        "ms_per_step": round(ms, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8 KV widened to fp16 / fp16 MFMA / fp32 accumulate",
-        "data": "synthetic (seeded N(0,1) K/V quantised absmax/127, fp16-valued Q, random page permutation)",
-        "config": {"workload": f"chunked prefill: 1 seq, {sq}-token causal chunk over {ctx} cached tokens "
-                               f"({ctx + sq} keys), 24 q / 4 kv heads, head_dim 256, int8 per-token-head "
-                               f"paged KV, block_size 16", "flops": flops, "rotating_caches": R},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_FP16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "pd_prefill_kernel", "avg_launch_us": round(ms * 1e3, 2)},
-        "cpu_baseline": cpu,
-    }
-    print(json.dumps(line))
+    once()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    sample_flops = 4 * 256 * 24 * sum(min(ctx + sq, ctx + r + 1) for r in rows)
+    return {"TFLOP_s": round(sample_flops / med / 1e12, 6), "cores": os.cpu_count(), "kind": "port",
+            "sample": f"float64 numpy oracle (oracle/attention.py paged_prefill) on {len(rows)} of the {sq} query "
+                      f"rows (all 24 heads, full visible context each), median of 3 runs after 1 warm-up, BLAS "
+                      f"threads on {os.cpu_count()} cores ({cpu_model()})",
+            "est_ms_full_chunk": round(flops / (sample_flops / med) * 1e3, 1)}
 
 
 if __name__ == "__main__":

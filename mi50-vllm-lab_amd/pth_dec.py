@@ -240,3 +240,12 @@ def launch_combine(seq_lens, query_start_loc, part_o, part_m, part_l, out, *, nu
 
 def version() -> str:
     return load_library().pth_dec_version().decode()
+
+
+def partial_kernel_name(rows_per_kv_head: int, block_size: int) -> str:
+    """Name of the split-K partial kernel a decode launch with this many query rows per kv head
+    (qmax * Hq / Hkv) and this block size runs (as rocprofv3 reports it, template arguments
+    included)."""
+    nrb = (rows_per_kv_head + 15) // 16
+    fast = block_size % 16 == 0
+    return f"pd_partial_kernel<{nrb}, {'true' if fast else 'false'}>"

@@ -108,6 +108,13 @@ def decode_splits(nseg: int, window: int, num_kv_heads: int, num_seqs: int, devi
     return best_s
 
 
+def _capturing(device) -> bool:
+    """True while a HIP graph is being captured on the current stream of `device`."""
+    if torch.device(device).type != "cuda":
+        return False
+    return bool(torch.cuda.is_current_stream_capturing())
+
+
 class _Operators:
     """The operator entry points the shim calls (the reference's torch-extension modules)."""
 
@@ -214,6 +221,11 @@ class Gfx950Int8Attention:
                 or query.shape[0] > segm_o.shape[0] or query.dim() != 3 or output.dim() != 3
                 or query.stride(1) != query.shape[2] or query.stride(2) != 1 or output.stride(2) != 1):
             return False
+        # Under graph capture the host lengths describe the capture's dummy batch, not the batches
+        # the graph will replay: size the split without them (the cap, or one round of workgroups
+        # for windowed rows).
+        if seq_lens_host is not None and _capturing(query.device):
+            seq_lens_host = None
         self.pth_dec.decode(query, key_cache, value_cache, k_scale_cache, v_scale_cache, block_table, seq_lens,
                             query_start_loc, output, self.scale, segm_o, meta.softmax_segm_max,
                             meta.softmax_segm_expsum, seq_lens.shape[0], max(1, max_q),

@@ -17,7 +17,6 @@ all checked against numbers that cannot drift with them:
 This code shares nothing with oracle/attention.py beyond the cache views. Re-running it must
 reproduce the committed file bit for bit (the generators are seeded CPU generators).
 """
-import importlib.util
 import math
 import os
 import sys
@@ -27,16 +26,14 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
-PKG = os.path.join(ROOT, "mi50-vllm-lab_amd")
 
 
 def _kvcache():
-    name = "_golden_kvcache"
-    spec = importlib.util.spec_from_file_location(name, os.path.join(PKG, "kvcache.py"))
-    m = importlib.util.module_from_spec(spec)
-    sys.modules[name] = m
-    spec.loader.exec_module(m)
-    return m
+    """The seeded workload generator of the tests (tests/workload.py)."""
+    sys.path.insert(0, os.path.dirname(HERE))
+    import workload
+
+    return workload
 
 
 CASES = {

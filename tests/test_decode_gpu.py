@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-import mi50_vllm_lab_amd.kvcache as kvc
+import workload as kvc
 from mi50_vllm_lab_amd import pth_dec
 from oracle import attention as orc
 
@@ -285,3 +285,59 @@ def test_hip_graph_capture_and_replay():
         torch.cuda.synchronize()
         say(f"graph replay {rep}")
         assert torch.equal(got.view(torch.int16), out.view(torch.int16))
+
+
+def test_config4_graph_replayed_1000_times():
+    """Config 4 as specified: the long-context call (200,000 keys, 1 % outlier rows) captured once in
+    a HIP graph and replayed 1,000 times. Every 250th replay is compared with the eager call (bit
+    for bit) after a device synchronisation; the last one is also held to the oracle."""
+    c = baseline_case(4)
+    ref, written = oracle_of(c)
+    d = c.to("cuda")
+    T = d.num_tokens
+    eager = gpu_decode(d, 64)
+    out = torch.zeros((T, HQ, 256), dtype=torch.float16, device="cuda")
+    po, pm, pl = kvc.partial_buffers(T, HQ, NSEG, "cuda")
+
+    def run():
+        pth_dec.decode(d.q, d.cache.key_cache, d.cache.value_cache, d.cache.k_scale, d.cache.v_scale, d.block_table,
+                       d.seq_lens, d.query_start_loc, out, d.scale, po, pm, pl, 1, 4, 64)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    torch.cuda.synchronize()
+    for rep in range(1, 1001):
+        graph.replay()
+        if rep % 250 == 0:
+            torch.cuda.synchronize()
+            say(f"config 4 graph replay {rep}")
+            assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), rep
+            out.zero_()
+            torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    emax, emean = errors(out, ref, written)
+    say(f"  last replay: max-abs {emax:.2e} mean-abs {emean:.2e}")
+    assert emax <= 2e-3 and emean <= 2e-4
+
+
+@pytest.mark.parametrize("nsplit", [1, 3])
+def test_48_rows_long_splits_scalar_block_table(nsplit):
+    """48 rows per kv head (three row blocks) over 20,000 keys with no window: at 1 and 3 splits a
+    split holds more tiles than the block-table slice the kernel stages in LDS, so the tile loop
+    looks pages up with scalar loads."""
+    c = kvc.make_case([20000], [8], num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=4848)
+    ref, written = oracle_of(c)
+    d = c.to("cuda")
+    say(f"48 rows, 20000 keys, nsplit {nsplit}")
+    out = gpu_decode(d, nsplit)
+    emax, emean = errors(out, ref, written)
+    say(f"  max-abs {emax:.2e} mean-abs {emean:.2e}")
+    assert emax <= 2e-3 and emean <= 2e-4

@@ -14,7 +14,7 @@ import re
 import pytest
 import torch
 
-import mi50_vllm_lab_amd.kvcache as kvc
+import workload as kvc
 from mi50_vllm_lab_amd import pth_dec
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))

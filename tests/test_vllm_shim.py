@@ -149,6 +149,23 @@ def test_route_passes_host_lengths_to_the_split_model(ops):
     assert ops.calls[-1][4] == 64
 
 
+def test_graph_capture_ignores_host_lengths(ops, monkeypatch):
+    """vLLM captures decode graphs with short dummy lengths: a split count fitted to them would be
+    frozen into the graph and replayed on long contexts. While capturing, the split is sized
+    without host lengths (the cap; one round of workgroups for windowed rows)."""
+    nseq = 8
+    q, out, kc = tensors(nseq)
+    m = meta([1] * nseq, [1] * nseq)
+    m.seq_lens_cpu = [1] * nseq
+    assert impl().route(q, kc, kc, None, None, m, out, 1, nseq, lambda *x: pytest.fail("fallback"))
+    assert ops.calls[-1][4] == 1  # eager: the model fits the short lengths
+    monkeypatch.setattr(shim, "_capturing", lambda device: True)
+    assert impl().route(q, kc, kc, None, None, m, out, 1, nseq, lambda *x: pytest.fail("fallback"))
+    assert ops.calls[-1][4] == 64  # captured: the cap, whatever the dummy lengths
+    assert impl(sliding_window=(2047, -1)).route(q, kc, kc, None, None, m, out, 1, nseq, lambda *x: None)
+    assert ops.calls[-1][4] == 256 // (4 * nseq)  # windowed: one round of workgroups
+
+
 @pytest.mark.parametrize("why", ["no_segm", "too_many_tokens", "q_stride", "layout", "mid_q", "noncausal"])
 def test_decode_fallbacks(monkeypatch, why):
     f = FakeOps(layout_ok=why != "layout")

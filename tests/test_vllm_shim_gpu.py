@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-import mi50_vllm_lab_amd.kvcache as kvc
+import workload as kvc
 from mi50_vllm_lab_amd import vllm_shim as shim
 from oracle import attention as orc
 
