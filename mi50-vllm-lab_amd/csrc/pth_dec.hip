@@ -115,8 +115,9 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kBtCache = 1024;                     // block-table entries of a split kept in LDS
 // With Q staged in LDS as well (block sizes that are multiples of 16) the block-table slice
 // is smaller:
-constexpr int kBtEarly = 384;                      // per-block row offsets (192 tiles per split)
-constexpr int kBtRaw = 384;                        // raw block-table entries of the split
+constexpr int kBtEarly = 384;                      // per-block row offsets (48 tiles per wave)
+constexpr int kBtRaw = 384;                        // raw block-table entries (96 per wave)
+constexpr int kBtWave = kBtEarly / 4;              // 16-key blocks staged per wave
 
 struct PartialParams {
     const _Float16* q;
@@ -212,11 +213,11 @@ struct TileSrc {
 
 template <bool kFast, bool kLds, class P>
 __device__ __forceinline__ TileSrc tile_src(const P& a, const PageTable& pt, const int8_t* gbase,
-                                            int tile, int tb, int lo, int hi, int lane) {
+                                            int tile, int idx, int lo, int hi, int lane) {
     if constexpr (kFast && kLds) {
-        // precomputed when the split started: one LDS read, no address arithmetic. The halves
-        // are zero-extended (readfirstlane returns a signed int).
-        const ull2_t r2 = pt.rows16[tile - tb];
+        // precomputed when the wave started (entry idx = the wave's tile number): one LDS read,
+        // no address arithmetic. The halves are zero-extended (readfirstlane returns a signed int).
+        const ull2_t r2 = pt.rows16[idx];
         const uint64_t o0 = ((uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((unsigned)(r2.x >> 32)) << 32) |
                             (uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((unsigned)r2.x);
         const uint64_t o1 = ((uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((unsigned)(r2.y >> 32)) << 32) |
@@ -416,9 +417,10 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     asm volatile("" ::"s"(a.qsl), "s"(a.seq_lens), "s"(a.block_table), "s"(a.bt_stride), "s"(a.kc), "s"(a.k_sb),
                  "s"(a.k_ss), "s"(a.k_sh), "s"(a.q), "s"(a.q_st), "s"(a.qmax), "s"(a.G), "s"(a.window),
                  "s"(a.nsplit), "s"(a.block_size), "s"(a.bs_shift));
-    const int q0 = a.qsl[b];
-    const int q_end = a.qsl[b + 1];
-    const int seq_len = a.seq_lens[b];
+    // (read-only for the kernel's lifetime: scalar loads through the constant address space)
+    const int q0 = ((const_int_ptr)(uintptr_t)a.qsl)[b];
+    const int q_end = ((const_int_ptr)(uintptr_t)a.qsl)[b + 1];
+    const int seq_len = ((const_int_ptr)(uintptr_t)a.seq_lens)[b];
     asm volatile("" ::"s"(q0), "s"(q_end), "s"(seq_len));
     const int q_len = q_end - q0;
     if (q_len <= 0 || seq_len <= 0) return;
@@ -430,16 +432,25 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     const int hi = seq_len;
     const int t_first = lo / kTile;
     const int ntiles = (hi - 1) / kTile - t_first + 1;
+    // Tiles of each wave. Split s owns a contiguous run of tiles [tb, te) and its waves take every
+    // kWaves-th tile of it, unless the block size is a multiple of 16 and there are at least as
+    // many tiles as the W = kWaves * nsplit waves of a (sequence, kv head): then the waves
+    // interleave over all the tiles, wave gw = kWaves * s + w taking tiles t_first + gw + W n, so
+    // that every split has work and the waves' counts differ by at most one. (Fewer tiles than
+    // waves: the contiguous runs measured faster, fewer workgroups with more waves busy.)
     const int per_split = (ntiles + a.nsplit - 1) / a.nsplit;
     const int tb = t_first + s * per_split;
     const int te = min(t_first + ntiles, tb + per_split);
+    const int W = kWaves * a.nsplit, gw = kWaves * s + w;
+    const bool interleave = kFast && ntiles >= W;
+    const bool empty = interleave ? kWaves * s >= ntiles : tb >= te;
 
     auto prow = [&](int r) -> int64_t {  // partial row index of query row r
         const int i = r / G, hh = r - i * G;
         return ((int64_t)(q0 + i) * a.Hq + (g * G + hh)) * a.nseg + s;
     };
 
-    if (tb >= te) {  // no tiles: mark the split empty for the combine
+    if (empty) {  // no tiles: mark the split empty for the combine
         for (int r = tid; r < R; r += kThreads) {
             a.part_m[prow(r)] = kNegInf;
             a.part_l[prow(r)] = 0.f;
@@ -447,8 +458,9 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         return;
     }
 
-    const int nt = max(0, (te - tb - w + kWaves - 1) / kWaves);  // tiles of this wave
-    auto tile_of = [&](int n) { return tb + w + kWaves * n; };
+    const int nt = interleave ? (gw < ntiles ? (ntiles - 1 - gw) / W + 1 : 0)
+                              : max(0, (te - tb - w + kWaves - 1) / kWaves);  // tiles of this wave
+    auto tile_of = [&](int n) { return interleave ? t_first + gw + W * n : tb + w + kWaves * n; };
 
     lds_u8* L = (lds_u8*)lds;
     const unsigned lds_base = (unsigned)(uintptr_t)L;
@@ -471,7 +483,7 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     PageTable pt;
     pt.glob = bt_row;
     pt.lds = (const lds_int*)(L + kLdsBt);
-    pt.rows16 = (const lds_ull2*)(L + kLdsBt);
+    pt.rows16 = (const lds_ull2*)(L + kLdsBt + (kEarly ? w * kBtWave * 8 : 0));
     pt.pfirst = max(tb * kTile, lo) / a.block_size;
 
     // ---- Q^T operand (B of S^T = K Q^T) of every row block; lane (lg, li) holds row 16 rb + li,
@@ -514,12 +526,17 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
 
     // ---- block-table slice of the split into LDS ----
     if constexpr (kEarly) {
-        const int pk_first = max(tb * kTile, lo), pk_last = min(te * kTile, hi) - 1;
-        const int plast = pk_last / a.block_size;
-        const int npages = plast - pt.pfirst + 1;
-        const int nblk = 2 * (te - tb);
-        pt.in_lds = nblk <= kBtEarly && npages <= kBtRaw;
-        (void)pk_first;
+        // the wave's own blocks (two per tile) are staged in its part of the table
+        const int nblk = 2 * nt;
+        pt.in_lds = nblk <= kBtWave;
+        // block j of this wave: the first key of its 16-key block clamped into the tile's visible
+        // keys (the tile_src rule), and that key's page
+        auto wave_block = [&](int j, int& key0, int& lb) {
+            const int kb = tile_of(j >> 1) * kTile;
+            const int kfirst = max(kb, lo), klast = min(kb + kTile - 1, hi - 1);
+            key0 = min(max(kb + 16 * (j & 1), kfirst), klast) & ~15;
+            lb = a.bs_shift >= 0 ? key0 >> a.bs_shift : key0 / a.block_size;
+        };
         // (0) the block-table entries of this wave's first two tiles (scalar loads), requested
         //     before any copy so that they do not queue behind the kernel's first copies
         //     (all four entries in one round trip; the tile_src rule, keys clamped into the tile's
@@ -544,8 +561,8 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
             else
                 src1.base[i - 2] = base;
         }
-        // (1) Q rows (two 512-byte rows per copy; rows past R repeat row R - 1) and the raw
-        //     block-table entries [pfirst, plast], spread over the waves
+        // (1) Q rows (two 512-byte rows per copy; rows past R repeat row R - 1), spread over the
+        //     waves, and the raw block-table entries of each wave's blocks
         const int nq = (R + 1) / 2;
         for (int i = w; i < nq; i += kWaves) {
             const int r = min(2 * i + (l >> 5), R - 1);
@@ -557,8 +574,13 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         }
         if (pt.in_lds) {
             const int* bt_glob = a.block_table + (int64_t)b * a.bt_stride;
-            for (int i = w; 64 * i < npages; i += kWaves)
-                dma4_v(bt_glob + min(pt.pfirst + 64 * i + l, plast), lds_base + (unsigned)(kLdsRaw + 256 * i));
+            for (int j0 = 0; j0 < nblk; j0 += 64) {
+                if (j0 + l < nblk) {  // lanes past the wave's blocks write nothing
+                    int key0, lb;
+                    wave_block(j0 + l, key0, lb);
+                    dma4_v(bt_glob + lb, lds_base + (unsigned)(kLdsRaw + 4 * (w * kBtWave + j0)));
+                }
+            }
         }
         // (2) this wave's first tile
         if (nt > 0) issue_tile<kFast>(a, src0, dl, wslots, l);
@@ -576,15 +598,13 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         else
             wait_vm<0>();
         __syncthreads();
-        if (pt.in_lds) {
-            const lds_int* raw = (const lds_int*)(L + kLdsRaw);
-            lds_u64* dst = (lds_u64*)(L + kLdsBt);
-            for (int i = tid; i < nblk; i += kThreads) {
-                const int kb = (tb + (i >> 1)) * kTile;
-                const int kfirst = max(kb, lo), klast = min(kb + kTile - 1, hi - 1);
-                const int key0 = min(max(kb + 16 * (i & 1), kfirst), klast) & ~15;
-                const int lb = key0 / a.block_size;
-                dst[i] = (uint64_t)((int64_t)raw[lb - pt.pfirst] * a.k_sb + (int64_t)(key0 - lb * a.block_size) * a.k_ss);
+        if (pt.in_lds) {  // the wave's own entries have landed (the wait above): row offsets
+            const lds_int* raw = (const lds_int*)(L + kLdsRaw) + w * kBtWave;
+            lds_u64* dst = (lds_u64*)(L + kLdsBt) + w * kBtWave;
+            for (int j = l; j < nblk; j += 64) {
+                int key0, lb;
+                wave_block(j, key0, lb);
+                dst[j] = (uint64_t)((int64_t)raw[j] * a.k_sb + (int64_t)(key0 - lb * a.block_size) * a.k_ss);
             }
         }
 #pragma unroll
@@ -846,7 +866,7 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         constexpr bool kLds = decltype(lds_flag)::value;
         auto issue = [&](int n) __attribute__((always_inline)) {
             wait_lds();  // every LDS access to the slot being refilled has completed
-            issue_tile<kFast>(a, tile_src<kFast, kLds>(a, pt, gbase, tile_of(n), tb, lo, hi, l), dl,
+            issue_tile<kFast>(a, tile_src<kFast, kLds>(a, pt, gbase, tile_of(n), n, lo, hi, l), dl,
                               wslots + (unsigned)((n & 1) * kSlot), l);
         };
         // The same copies in two parts (16-key row blocks): the 8 K blocks, then the 8 V blocks
@@ -854,7 +874,7 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         TileSrc nsrc;
         auto issue_k = [&](int n) __attribute__((always_inline)) {
             wait_lds();  // every LDS access to the slot being refilled has completed
-            nsrc = tile_src<kFast, kLds>(a, pt, gbase, tile_of(n), tb, lo, hi, l);
+            nsrc = tile_src<kFast, kLds>(a, pt, gbase, tile_of(n), n, lo, hi, l);
             const unsigned slot = wslots + (unsigned)((n & 1) * kSlot);
 #pragma unroll
             for (int i = 0; i < 8; ++i)
@@ -1569,7 +1589,7 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
                 src.base[0] = gbase + ((int64_t)o0 << 3);
                 src.base[1] = gbase + ((int64_t)o1 << 3);
             } else {
-                src = tile_src<kFast, kLds>(a, pt, gbase, n, 0, 0, hi, l);
+                src = tile_src<kFast, kLds>(a, pt, gbase, n, n, 0, hi, l);
             }
             const unsigned slot = lds_base + kLdsRaw + (unsigned)((n & (kFaRaw - 1)) * kSlot);
             wait_lds();
