@@ -101,6 +101,23 @@ hipError_t pth_dec_launch_combine(const int* seq_lens, const int* qsl, int num_s
                                   const float* part_l, int nseg, int nsplit, void* out, long o_st,
                                   long o_sh, hipStream_t stream);
 
+/*
+ * pth_dec_launch_window without the partial buffers, for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. The split partials go to a device array the library holds (32 MiB
+ * per GPU, for the life of the process); this call allocates nothing. Limit:
+ * num_tokens * heads_q * nsplit * 1032 bytes <= 32 MiB (e.g. 4 tokens x 24 heads x 64 splits);
+ * beyond it the call returns hipErrorOutOfMemory and launches nothing. Other checks and errors
+ * as pth_dec_launch_window. Every call on a GPU shares that GPU's array: calls that overlap on
+ * one GPU (different streams) race; calls on one stream are ordered and safe.
+ */
+hipError_t pth_dec_launch_noalloc(const void* q, int q_st, const void* kc, int k_sb, int k_ss, int k_sh,
+                                  const int* block_table, int bt_stride, const int* seq_lens,
+                                  const int* qsl, int num_seqs, int num_tokens, int heads_q,
+                                  int heads_kv, int block_size, float scale, int qmax, int nsplit,
+                                  void* out, long o_st, long o_sh, hipStream_t stream, int window,
+                                  int causal);
+
 /* 1 if the four cache views have the row layout above, else 0 (pth_dec.cpp:25-41). */
 int pth_dec_supported_layout(const pd_tensor* key_cache, const pd_tensor* value_cache,
                              const pd_tensor* k_scale, const pd_tensor* v_scale);

@@ -60,6 +60,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "pth_dec.h"
@@ -1943,6 +1945,38 @@ int fail(char* err, int errlen, const char* msg) {
     return 1;
 }
 
+// Partials of pth_dec_launch_noalloc: part_o [T, Hq, nsplit, 256], then part_m and part_l
+// [T, Hq, nsplit], in device memory the library holds (one copy per GPU, for the life of the
+// process). Host code never passes `scratch` itself to a kernel (on the host it only names the
+// symbol): each device's address comes from hipGetSymbolAddress, once per device.
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Address of the current device's scratch array (looked up on its first use on that device).
+hipError_t scratch_address(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+        if (p == nullptr) {
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess) return e;
+            if (p == nullptr) return hipErrorInvalidSymbol;
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return hipSuccess;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1968,6 +2002,31 @@ hipError_t pth_dec_launch_window(const void* q, int q_st, const void* kc, int k_
                                    num_tokens, heads_q, heads_kv, block_size, scale, qmax, part_o, part_m, part_l,
                                    nseg, nsplit, out, o_st, o_sh, window, causal);
     return launch_all(x, stream, false);
+}
+
+hipError_t pth_dec_launch_noalloc(const void* q, int q_st, const void* kc, int k_sb, int k_ss, int k_sh,
+                                  const int* block_table, int bt_stride, const int* seq_lens,
+                                  const int* qsl, int num_seqs, int num_tokens, int heads_q,
+                                  int heads_kv, int block_size, float scale, int qmax, int nsplit,
+                                  void* out, long o_st, long o_sh, hipStream_t stream, int window,
+                                  int causal) {
+    LaunchArgs x = make_args(q, q_st, kc, k_sb, k_ss, k_sh, block_table, bt_stride, seq_lens, qsl, num_seqs,
+                             num_tokens, heads_q, heads_kv, block_size, scale, qmax, nullptr, nullptr, nullptr,
+                             nsplit, nsplit, out, o_st, o_sh, window, causal);
+    hipError_t e = check_args(x, false);
+    if (e != hipSuccess) return e;
+    if (num_tokens == 0) return hipSuccess;
+    const size_t rows = (size_t)num_tokens * (size_t)heads_q * (size_t)nsplit;
+    if (rows * (kDim + 2) * sizeof(float) > kScratchBytes) return hipErrorOutOfMemory;
+    void* base = nullptr;
+    e = scratch_address(&base);
+    if (e != hipSuccess) return e;
+    x.part_o = static_cast<float*>(base);
+    x.part_m = x.part_o + rows * kDim;
+    x.part_l = x.part_m + rows;
+    e = launch_partial(x, stream);
+    if (e != hipSuccess) return e;
+    return launch_combine(x, stream);
 }
 
 hipError_t pth_dec_launch_partial(const void* q, int q_st, const void* kc, int k_sb, int k_ss, int k_sh,

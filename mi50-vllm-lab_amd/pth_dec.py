@@ -42,6 +42,7 @@ _DTYPES = {
 EXPORTED_SYMBOLS = (
     "pth_dec_launch",
     "pth_dec_launch_window",
+    "pth_dec_launch_noalloc",
     "pth_dec_launch_partial",
     "pth_dec_launch_combine",
     "pth_dec_supported_layout",
@@ -86,6 +87,9 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.pth_dec_launch.restype = c_int
     lib.pth_dec_launch_window.argtypes = launch_args + [c_int, c_int]
     lib.pth_dec_launch_window.restype = c_int
+    lib.pth_dec_launch_noalloc.argtypes = [vp, c_int, vp, c_int, c_int, c_int, ip, c_int, ip, ip, c_int, c_int, c_int,
+                                           c_int, c_int, c_float, c_int, c_int, vp, c_long, c_long, vp, c_int, c_int]
+    lib.pth_dec_launch_noalloc.restype = c_int
     lib.pth_dec_launch_partial.argtypes = [vp, c_int, vp, c_int, c_int, c_int, ip, c_int, ip, ip, c_int, c_int,
                                            c_int, c_int, c_int, c_float, c_int, fp, fp, fp, c_int, c_int, vp,
                                            c_int, c_int]
