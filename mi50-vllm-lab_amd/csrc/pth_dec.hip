@@ -1248,7 +1248,16 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
     static_assert(kLdsBytes <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
     __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
 
-    const int qt = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    // Workgroups are dispatched to the 8 XCDs round robin (linear id L to XCD L % 8), and each XCD
+    // has its own L2. Every query tile of a (sequence, kv head) streams the same keys, so the
+    // logical workgroup index (query tile fastest) is laid out XCD by XCD: XCD x takes a
+    // contiguous range of it, and the query tiles sharing a kv head mostly share an L2 (config 5:
+    // each kv head's 64 query tiles on two XCDs).
+    const unsigned nx = gridDim.x, ny = gridDim.y, nwg = nx * ny * gridDim.z;
+    const unsigned lin = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+    const unsigned xcd = lin % 8u;
+    const unsigned lidx = xcd * (nwg / 8u) + min(xcd, nwg % 8u) + lin / 8u;
+    const int qt = (int)(lidx % nx), g = (int)((lidx / nx) % ny), b = (int)(lidx / (nx * ny));
     const int tid = threadIdx.x, l = tid & 63, lg = l >> 4, li = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = a.G;
