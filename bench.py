@@ -107,6 +107,41 @@ def summarize_traffic(args):
     print(json.dumps(summary))
 
 
+COUNTERS = ("SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_MFMA", "SQ_WAVES", "SQ_BUSY_CU_CYCLES",
+            "SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE")
+
+
+def summarize_counters(args):
+    """Instruction mix and MFMA utilisation per partial-kernel launch from one rocprofv3 --pmc run
+    of --profile-only with COUNTERS (medians over the dispatches), per wave and per 32-key tile."""
+    per = {c: _pmc_dispatches(args.counters_summary, c) for c in COUNTERS}
+    med = {}
+    for c, d in per.items():
+        v = sorted(x for name, x in d.values() if "partial" in name)
+        if not v:
+            raise SystemExit(f"{c}: no partial-kernel dispatches")
+        med[c] = v[len(v) // 2]
+    import workload as wl
+
+    case = decode_case(wl, 2)
+    tiles = 4 * (((case.seq_lens[0].item() - 1) // 32) + 1)  # 32-key tiles over the 4 kv heads
+    waves = med["SQ_WAVES"]
+    simd_cycles = med["SQ_BUSY_CU_CYCLES"] / 256 * 1.0  # per CU: 4 SIMDs, each busy that long
+    summary = {
+        "kernel": "decode partial kernel", "workload": "MTP verify 4 x 24/4 heads, ctx 61440+4, bs 16",
+        "nsplit": args.nsplit, "counters_median_per_dispatch": {c: round(v) for c, v in med.items()},
+        "per_wave": {c: round(med[c] / waves, 1) for c in ("SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_MFMA")},
+        "per_tile": {c: round(med[c] / tiles, 1) for c in ("SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_MFMA")},
+        "tiles": tiles,
+        "mfma_busy": round(med["SQ_VALU_MFMA_BUSY_CYCLES"] / (4 * 256 * simd_cycles), 4),
+        "note": "SQ_INSTS_VALU includes the MFMA instructions; mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / "
+                "(1024 SIMDs x SQ_BUSY_CU_CYCLES / 256 CUs)",
+    }
+    with open(args.counters_out, "w") as f:
+        json.dump(summary, f, indent=1)
+    print(json.dumps(summary))
+
+
 def load_package():
     import importlib.util
 
@@ -275,10 +310,20 @@ def main():
                     help="no GPU work: turn two rocprofv3 --pmc runs of --profile-only (FETCH_SIZE, WRITE_SIZE) "
                          "into HBM bytes per partial launch, written to --traffic-out")
     ap.add_argument("--traffic-out", default=os.path.join(PROFILES, "pd_partial_mtp61k_traffic.json"))
+    ap.add_argument("--profile-prefill", type=int, default=0, metavar="N",
+                    help="run N config-5 prefill chunks (alternating two cache copies) and nothing else, for "
+                         "rocprofv3")
+    ap.add_argument("--counters-summary", metavar="PMC_DIR",
+                    help="no GPU work: turn a rocprofv3 --pmc run of --profile-only with the counters in "
+                         "bench.COUNTERS into instruction mix and MFMA utilisation, written to --counters-out")
+    ap.add_argument("--counters-out", default=os.path.join(PROFILES, "pd_partial_mtp61k_counters.json"))
     args = ap.parse_args()
 
     if args.traffic_summary:
         summarize_traffic(args)
+        return
+    if args.counters_summary:
+        summarize_counters(args)
         return
 
     if args.gpus != 1:
@@ -300,6 +345,12 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream()
+
+    if args.profile_prefill:
+        res = bench_prefill(torch, wl, pd, dev, stream, reps=2 * max(1, args.profile_prefill // 2))
+        print(json.dumps({"profile_prefill": True, "chunks": 2 * max(1, args.profile_prefill // 2) + 4,
+                          "ms_per_chunk": res["ms_per_chunk"]}))
+        return
 
     case2 = decode_case(wl, 2)
     b2 = DecodeBench(torch, wl, pd, dev, case2, args.rotate, args.nsplit)
