@@ -15,12 +15,16 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB_DIR = os.path.join(HERE, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libpthdec.so")
-SOURCES = [os.path.join(HERE, "csrc", "pth_dec.hip")]
+# the C ABI, then the kernels (each file compiles on its own; they share csrc/pd_*.hpp)
+SOURCES = [os.path.join(HERE, "csrc", f) for f in
+           ("pd_api.hip", "pd_decode.hip", "pd_prefill.hip", "pd_cache_write.hip")]
+KERNEL_SOURCES = SOURCES[1:]
 ARCH = "gfx950"
 
-# Packed-FP32 VALU forms are disabled for all device code built here.
+# Packed-FP32 VALU forms are disabled for all device code built here. Symbols are hidden
+# unless pd_api.hip exports them (the entry points of include/pth_dec.h).
 HIP_FLAGS = [
-    "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-fPIC", "-shared",
+    "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-fPIC", "-shared", "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
 ]

@@ -2,7 +2,7 @@
 
 Every kernel of libpthdec.so must run without scratch memory: a spill to scratch in the decode
 or prefill kernels costs a memory round trip per spilled value inside the tile loop. The check
-compiles the library source to gfx950 assembly with the flags of the product build and reads
+compiles each kernel source to gfx950 assembly with the flags of the product build and reads
 each kernel's `.private_segment_fixed_size` from the code-object metadata.
 """
 import os
@@ -15,7 +15,6 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG_DIR = os.path.join(ROOT, "mi50-vllm-lab_amd")
-SOURCE = os.path.join(PKG_DIR, "csrc", "pth_dec.hip")
 
 
 def _hipcc():
@@ -36,23 +35,28 @@ def gfx950_asm(tmp_path_factory):
     finally:
         sys.path.remove(PKG_DIR)
     flags = [f for f in pd_build.HIP_FLAGS if f not in ("-shared", "-fPIC")]
-    out = str(tmp_path_factory.mktemp("asm") / "pth_dec.s")
-    cmd = [hipcc, *flags, "--cuda-device-only", "-S", "-I", os.path.join(ROOT, "include"), SOURCE, "-o", out]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    assert res.returncode == 0, res.stderr[-4000:]
-    with open(out) as f:
-        return f.read()
+    tmp = tmp_path_factory.mktemp("asm")
+    text = []
+    for src in pd_build.KERNEL_SOURCES:
+        out = str(tmp / (os.path.basename(src) + ".s"))
+        cmd = [hipcc, *flags, "--cuda-device-only", "-S", "-I", os.path.join(ROOT, "include"), src, "-o", out]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        assert res.returncode == 0, (src, res.stderr[-4000:])
+        with open(out) as f:
+            text.append(f.read())
+    return text
 
 
-def _kernel_metadata(asm):
-    """{kernel name: metadata text} from the amdhsa.kernels list of the code object."""
-    meta = asm[asm.index("amdhsa.kernels:"):]
-    entries = re.split(r"\n  - ", meta)
+def _kernel_metadata(asms):
+    """{kernel name: metadata text} from the amdhsa.kernels lists of the code objects."""
     out = {}
-    for e in entries[1:]:
-        m = re.search(r"\.name:\s+(\S+)", e)
-        if m:
-            out[m.group(1)] = e
+    for asm in asms:
+        meta = asm[asm.index("amdhsa.kernels:"):]
+        entries = re.split(r"\n  - ", meta)
+        for e in entries[1:]:
+            m = re.search(r"\.name:\s+(\S+)", e)
+            if m:
+                out[m.group(1)] = e
     return out
 
 
@@ -76,4 +80,5 @@ def test_no_kernel_uses_scratch(gfx950_asm):
 
 def test_no_packed_fp32_instructions(gfx950_asm):
     # the build disables the packed-FP32 VALU forms; none may appear in the code
-    assert not re.search(r"\bv_pk_(add|mul|fma)_f32\b", gfx950_asm)
+    for asm in gfx950_asm:
+        assert not re.search(r"\bv_pk_(add|mul|fma)_f32\b", asm)

@@ -8,8 +8,9 @@ calls reaches a device: every case here fails validation or has no tokens.
 """
 import ctypes
 import os
-import shutil
 import re
+import shutil
+import subprocess
 
 import pytest
 import torch
@@ -53,6 +54,21 @@ def test_header_symbols_exported(lib):
     assert names == sorted(pth_dec.EXPORTED_SYMBOLS)
     for n in names:
         assert hasattr(lib, n), n
+
+
+def test_library_exports_only_the_entry_points(lib):
+    """Built with hidden visibility: besides the header's entry points the library exports only
+    what HIP itself keeps visible (the kernels' host stubs and the code objects' ids)."""
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    res = subprocess.run([nm, "-D", "--defined-only", pth_dec.LIB_PATH], capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+    names = {line.split()[-1] for line in res.stdout.splitlines() if line.strip()}
+    internal = {n for n in names if n not in pth_dec.EXPORTED_SYMBOLS and not n.startswith("__hip_cuid_")
+                and not (n.startswith("_ZN2pd") and "_kernel" in n) and n not in ("_init", "_fini")}
+    assert not internal, sorted(internal)
+    assert set(pth_dec.EXPORTED_SYMBOLS) <= names
 
 
 def test_version(lib):
