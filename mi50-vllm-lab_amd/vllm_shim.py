@@ -69,19 +69,25 @@ def cu_count(device) -> int:
 # Makespan model of the decode partial kernel (grid splits x kv heads x sequences, one
 # workgroup per CU), fitted to MI355X measurements: a workgroup costs ~12 us of set-up and merge
 # plus ~3.3 us per 32-key tile of its busiest wave (4 waves share a split's tiles); a split
-# with no tiles ~2 us.
+# with no tiles ~2 us. The combine after it reads every split's partial row (1,032 bytes per
+# (token, q head, split)) at ~4 TB/s: ~0.25 us per MB on top of a fixed cost that no split count
+# changes.
 SPLIT_FIXED_US, SPLIT_TILE_US, SPLIT_EMPTY_US = 12.0, 3.3, 2.0
+COMBINE_US_PER_MB = 0.25
+PARTIAL_ROW_BYTES = 1032
 
 
 def decode_splits(nseg: int, window: int, num_kv_heads: int, num_seqs: int, device, seq_lens_host=None,
-                  max_q: int = 1) -> int:
+                  max_q: int = 1, num_q_heads: Optional[int] = None) -> int:
     """Splits per sequence for the decode operator, at most min(VLLM_GFX950_PTH_DEC_SPLITS, nseg).
 
     With the host-side sequence lengths, the candidate (powers of two and the cap) with the
-    smallest modelled makespan max(total workgroup time / CUs, longest workgroup): few splits
-    for many sequences, many for one long sequence. Without them: a sliding window bounds every
-    sequence to about window + qmax keys, so the grid is sized to one workgroup per CU; otherwise
-    the cap (the reference's rule)."""
+    smallest modelled time: the partial kernel's makespan max(total workgroup time / CUs, longest
+    workgroup) plus the combine's reading of the partials (num_seqs x max_q x num_q_heads rows,
+    6 q heads per kv head when not given). Few splits for many sequences, many for one long
+    sequence. Without the lengths: a sliding window bounds every sequence to about window + qmax
+    keys, so the grid is sized to one workgroup per CU; otherwise the cap (the reference's
+    rule)."""
     cap = max(1, min(PTH_DEC_SPLITS, nseg))
     cus = cu_count(device)
     if seq_lens_host is None:
@@ -95,6 +101,7 @@ def decode_splits(nseg: int, window: int, num_kv_heads: int, num_seqs: int, devi
     live = tiles > 0
     if not live.any():
         return 1
+    rows = num_seqs * max(1, max_q) * (num_q_heads if num_q_heads else 6 * num_kv_heads)
     cands = sorted({1 << k for k in range(int(math.log2(cap)) + 1)} | {cap})
     best_s, best_t = cap, float("inf")
     for s in cands:
@@ -103,6 +110,7 @@ def decode_splits(nseg: int, window: int, num_kv_heads: int, num_seqs: int, devi
         t = SPLIT_FIXED_US + SPLIT_TILE_US * -(-per // 4)
         total = num_kv_heads * float(np.sum(n * t + (s - n) * SPLIT_EMPTY_US))
         span = max(total / cus, float(t[live].max()))
+        span += COMBINE_US_PER_MB * rows * s * PARTIAL_ROW_BYTES / 1e6
         if span < best_t - 1e-9:
             best_s, best_t = s, span
     return best_s
@@ -230,7 +238,7 @@ class Gfx950Int8Attention:
                             query_start_loc, output, self.scale, segm_o, meta.softmax_segm_max,
                             meta.softmax_segm_expsum, seq_lens.shape[0], max(1, max_q),
                             decode_splits(segm_o.shape[2], self.window, self.num_kv_heads, seq_lens.shape[0],
-                                          query.device, seq_lens_host, max(1, max_q)),
+                                          query.device, seq_lens_host, max(1, max_q), query.shape[1]),
                             window=self.window, causal=True)
         return True
 

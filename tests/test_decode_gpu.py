@@ -112,6 +112,77 @@ def test_baseline_configs(n, nsplit):
     assert emax <= 2e-3 and emean <= 2e-4, (n, emax, emean)
 
 
+def _key0_slot(c):
+    """Physical (block, slot) of sequence 0's key 0."""
+    return int(c.block_table[0, 0]), 0
+
+
+def test_widening_every_byte_value_as_v_bit_exact():
+    """All 256 int8 values through the device's int8 -> fp16 widening of V: with one visible key the
+    softmax weight is exactly 1, so out = V * v_scale must hold every value exactly (v_scale 2^-7
+    makes v / 128 an fp16 number). Kv head g holds value (d + 64 g) mod 256 - 128 at dim d, so
+    every value (0x80 included) sits at several dims and lane positions."""
+    c = kvc.make_case([0], [1], num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=41, kv_mode="uniform")
+    blk, slot = _key0_slot(c)
+    d = torch.arange(256)
+    for g in range(HKV):
+        v = ((d + 64 * g) % 256 - 128).to(torch.int8)
+        c.cache.value_cache[blk, slot, g, :256] = v
+        c.cache.v_scale[blk, slot, g] = 2.0 ** -7
+    say("widening: every byte value as V")
+    for ns in (1, 64):
+        out = gpu_decode(c.to("cuda"), ns).float().cpu()
+        for hq in range(HQ):
+            g = hq // (HQ // HKV)
+            want = ((d + 64 * g) % 256 - 128).float() / 128.0
+            assert torch.equal(out[0, hq], want), (ns, hq, (out[0, hq] - want).abs().max().item())
+
+
+def test_widening_every_byte_value_as_k():
+    """All 256 int8 values through the widening of K: key 0 of kv head g holds value
+    (72 g + d) mod 256 - 128 at dim d (k_scale 1/4, V = 1), the other keys are zero (V = 0), and
+    each query row is one-hot at one dim, so its output is e^s / (e^s + keys - 1) with s the
+    scaled value of one byte. Three calls of 24 rows per kv head reach dims 0..71 of every head,
+    which covers each of the 256 values. One unit of a byte moves s by 1/64, and so the row's
+    output by at least 0.3 % (relative; 1 - out >= 0.21 for s <= 2 and 3..6 visible keys), three
+    times the 2^-10 allowed. V = 1 is stored as the byte 127 with v_scale 1/127: the widened V
+    carries the +1152 bias, and a byte as small as 1 would make the fp32 sums of P'(v + 1152)
+    lose ~10 bits when the bias is removed (~1.5e-3 relative here), which is not what this test
+    is about."""
+    c = kvc.make_case([2], [4], num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=43, kv_mode="uniform")
+    seq = 6
+    bt = c.block_table[0].long()
+    pos = torch.arange(seq)
+    blk, slot = bt[pos // 16], pos % 16
+    dims = torch.arange(256)
+    c.cache.key_cache[blk, slot, :, :256] = 0
+    c.cache.value_cache[blk, slot, :, :256] = 0
+    c.cache.k_scale[blk, slot] = 1.0
+    c.cache.v_scale[blk, slot] = 1.0 / 127
+    b0, s0 = int(blk[0]), int(slot[0])
+    for g in range(HKV):
+        c.cache.key_cache[b0, s0, g, :256] = ((72 * g + dims) % 256 - 128).to(torch.int8)
+        c.cache.value_cache[b0, s0, g, :256] = 127
+        c.cache.k_scale[b0, s0, g] = 0.25
+    G = HQ // HKV
+    seen = set()
+    for call in range(3):
+        q = torch.zeros_like(c.q)
+        for t in range(4):
+            for hq in range(HQ):
+                j = t * G + hq % G
+                dim = 24 * call + j
+                q[t, hq, dim] = 1.0
+                seen.add((72 * (hq // G) + dim) % 256)
+        c.q = q
+        ref, written = oracle_of(c)
+        say(f"widening: every byte value as K, call {call}")
+        out = gpu_decode(c.to("cuda"), 1).double().cpu().numpy()
+        rel = np.abs(out - ref)[written] / np.abs(ref[written])
+        assert rel.max() <= 2.0 ** -10, (call, rel.max())
+    assert seen == set(range(256))
+
+
 def test_nan_poisoned_freed_pages_bit_exact():
     args = dict(num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=1003, causal=False, window=2048)
     ctxs, qlens = [2048, 9216, 33792, 122880], [8, 8, 8, 8]
