@@ -282,6 +282,49 @@ def decode_line(us, db):
             "tflops": round(db.flops / (us * 1e-6) / 1e12, 2)}
 
 
+# kernels/pth_dec/test_dec.py:150-165: (B, q_len) x ctx, cells with B * ctx > 270,000 skipped
+GRID = ((1, 4), (2, 4), (4, 4), (1, 1), (2, 1))
+GRID_CTX = (4096, 16384, 32768, 65536, 131072)
+
+
+def bench_grid(torch, wl, pd, shim, dev, stream, hq, hkv, block_size):
+    """The reference's decode speed grid at hq / hkv heads and the given block size: µs per layer
+    (whole operator) at the split count the vLLM shim picks and at 64, the reference's default.
+    Each cell cycles enough cache copies (>= 512 MiB) that every call reads its KV from HBM, not
+    from the 256 MB Infinity Cache; one line of JSON per cell."""
+    rows = []
+    for B, ql in GRID:
+        for ctx in GRID_CTX:
+            if B * ctx > 270000:
+                continue
+            c = wl.make_case([ctx] * B, [ql] * B, num_q_heads=hq, num_kv_heads=hkv, block_size=block_size, seed=1)
+            copies = max(2, min(64, -(-(512 << 20) // c.cache.nbytes())))
+            pick = shim.decode_splits(NSEG, -1, hkv, B, dev, c.seq_lens.tolist(), ql, hq)
+            cell = {"B": B, "q_len": ql, "ctx": ctx, "heads": f"{hq}/{hkv}", "block_size": block_size,
+                    "nsplit_pick": pick, "copies": copies}
+            for ns in sorted({pick, 64}):
+                db = DecodeBench(torch, wl, pd, dev, c, copies, ns)
+                with torch.cuda.stream(stream):
+                    for i in range(copies):
+                        db.op(i)()
+                torch.cuda.synchronize()
+                g = graph_of(torch, stream, [db.op(i) for i in range(copies)])
+                reps = max(3, 2000 // copies)
+                with torch.cuda.stream(stream):
+                    g.replay()
+                    ms = time_replays(torch, g, reps, stream)
+                us = ms * 1e3 / (reps * copies)
+                cell[f"us_ns{ns}"] = round(us, 2)
+                if ns == pick:
+                    cell["GB_s"] = round(db.alg_bytes / (us * 1e-6) / 1e9, 1)
+                del db, g
+                torch.cuda.empty_cache()
+            print(json.dumps(cell), flush=True)
+            rows.append(cell)
+            del c
+    return rows
+
+
 def committed_profile(name):
     p = os.path.join(PROFILES, name)
     if not os.path.exists(p):
@@ -317,6 +360,9 @@ def main():
                     help="no GPU work: turn a rocprofv3 --pmc run of --profile-only with the counters in "
                          "bench.COUNTERS into instruction mix and MFMA utilisation, written to --counters-out")
     ap.add_argument("--counters-out", default=os.path.join(PROFILES, "pd_partial_mtp61k_counters.json"))
+    ap.add_argument("--grid", metavar="HQ,HKV,BS",
+                    help="only the reference's decode speed grid (B x q_len x ctx) at HQ q heads, HKV kv heads "
+                         "and block size BS, one JSON line per cell")
     args = ap.parse_args()
 
     if args.traffic_summary:
@@ -345,6 +391,11 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream()
+
+    if args.grid:
+        hq, hkv, bs = (int(x) for x in args.grid.split(","))
+        bench_grid(torch, wl, pd, pkg.vllm_shim, dev, stream, hq, hkv, bs)
+        return
 
     if args.profile_prefill:
         res = bench_prefill(torch, wl, pd, dev, stream, reps=2 * max(1, args.profile_prefill // 2))
