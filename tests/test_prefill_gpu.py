@@ -194,11 +194,13 @@ def test_outlier_rows_within_fp16_weight_rounding():
 
 @pytest.mark.parametrize("bs", [16, 8])
 def test_page_table_beyond_lds(bs):
-    # more 16-key blocks (bs 16) or pages (bs 8) than the workgroup's LDS table holds
-    c = kvc.make_case([90000], [40], num_q_heads=HQ, num_kv_heads=HKV, block_size=bs, seed=21 + bs)
+    # more 16-key blocks (bs 16: 6,252) or pages (bs 8: 12,500) than the workgroup's LDS table
+    # holds (6,144 entries), so the tile addresses come from the global block table
+    ctx = 100000
+    c = kvc.make_case([ctx], [40], num_q_heads=HQ, num_kv_heads=HKV, block_size=bs, seed=21 + bs)
     say(f"prefill global page table bs={bs}")
-    out = gpu_prefill(c.to("cuda"), [90000])
-    ref, written = oracle_of(c, [90000], [0, 13, 39])
+    out = gpu_prefill(c.to("cuda"), [ctx])
+    ref, written = oracle_of(c, [ctx], [0, 13, 39])
     emax, emean = errors(out, ref, written)
     say(f"  max-abs {emax:.2e} mean-abs {emean:.2e}")
     assert emax <= 2e-3 and emean <= 2e-4, (emax, emean)
