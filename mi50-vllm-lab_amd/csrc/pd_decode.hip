@@ -121,52 +121,6 @@ struct TileOps {
     float vs[8];      // v_scale of the same keys
 };
 
-// acc *= alpha for MFMA accumulators, through LDS (16 bytes per lane and accumulator, 1 KiB
-// apart from `lds_addr`): the accumulators are read and written only by asm with AGPR operands.
-// Four at a time: two LDS round trips per four accumulators.
-__device__ __forceinline__ void agpr_scale4_via_lds(float4_t& a0, float4_t& a1, float4_t& a2, float4_t& a3,
-                                                    float alpha, unsigned lds_addr) {
-    float4_t t0, t1, t2, t3;
-    asm volatile(
-        "ds_write_b128 %4, %5\n\tds_write_b128 %4, %6 offset:1024\n\t"
-        "ds_write_b128 %4, %7 offset:2048\n\tds_write_b128 %4, %8 offset:3072\n\t"
-        "s_waitcnt lgkmcnt(0)\n\t"
-        "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:1024\n\t"
-        "ds_read_b128 %2, %4 offset:2048\n\tds_read_b128 %3, %4 offset:3072\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
-        : "v"(lds_addr), "a"(a0), "a"(a1), "a"(a2), "a"(a3)
-        : "memory");
-    t0 *= alpha;
-    t1 *= alpha;
-    t2 *= alpha;
-    t3 *= alpha;
-    asm volatile(
-        "ds_write_b128 %4, %5\n\tds_write_b128 %4, %6 offset:1024\n\t"
-        "ds_write_b128 %4, %7 offset:2048\n\tds_write_b128 %4, %8 offset:3072\n\t"
-        "s_waitcnt lgkmcnt(0)\n\t"
-        "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:1024\n\t"
-        "ds_read_b128 %2, %4 offset:2048\n\tds_read_b128 %3, %4 offset:3072\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&a"(a0), "=&a"(a1), "=&a"(a2), "=&a"(a3)
-        : "v"(lds_addr), "v"(t0), "v"(t1), "v"(t2), "v"(t3)
-        : "memory");
-}
-
-// The same for one accumulator.
-__device__ __forceinline__ void agpr_scale_via_lds(float4_t& acc, float alpha, unsigned lds_addr) {
-    float4_t t;
-    asm volatile("ds_write_b128 %1, %2\n\ts_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
-                 : "=v"(t)
-                 : "v"(lds_addr), "a"(acc)
-                 : "memory");
-    t *= alpha;
-    asm volatile("ds_write_b128 %1, %2\n\ts_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
-                 : "=a"(acc)
-                 : "v"(lds_addr), "v"(t)
-                 : "memory");
-}
-
 // One workgroup = kWaves independent waves. Wave w of split s streams tiles tb + w, tb + w + 4,
 // ... of the split and computes all R query rows of the kv head for each (NRB row blocks of
 // 16), so every K/V byte is loaded and widened once. Each wave double-buffers its tiles in LDS:
@@ -573,8 +527,9 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
 #pragma unroll
             for (int e = 0; e < 8; ++e) sv[rb][e] -= shift;
             l_run[rb] *= alpha;
-            // O is still zero while every row of the block is fresh: skip the rescale then
-            if (__builtin_amdgcn_ballot_w64(!fresh) != 0) {
+            // O is still zero while every row of the block is fresh, and a row that keeps its
+            // max would be multiplied by 1: rescale only when a row with state raises
+            if (__builtin_amdgcn_ballot_w64(raise && !fresh) != 0) {
                 if constexpr (NRB >= 3) {
 #pragma unroll
                     for (int m = 0; m < 16; m += 4)

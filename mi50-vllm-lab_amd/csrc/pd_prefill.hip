@@ -368,16 +368,14 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
 #pragma unroll
             for (int e = 0; e < 8; ++e) sv[rb][e] -= shift;
             l_run[rb] *= alpha;
-            if (__builtin_amdgcn_ballot_w64(!fresh) != 0) {
+            // O is still zero while every row of the block is fresh, and a row that keeps its
+            // max would be multiplied by 1: rescale only when a row with state raises, four
+            // accumulators per LDS round trip
+            if (__builtin_amdgcn_ballot_w64(raise && !fresh) != 0) {
 #pragma unroll
-                for (int m = 0; m < 17; ++m) {
-                    float4_t t;
-                    asm volatile("ds_write_b128 %1, %2\n\ts_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
-                                 : "=v"(t) : "v"(scr_addr), "a"(oacc[rb][m]) : "memory");
-                    t *= alpha;
-                    asm volatile("ds_write_b128 %1, %2\n\ts_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
-                                 : "=a"(oacc[rb][m]) : "v"(scr_addr), "v"(t) : "memory");
-                }
+                for (int m = 0; m < 16; m += 4)
+                    agpr_scale4_via_lds(oacc[rb][m], oacc[rb][m + 1], oacc[rb][m + 2], oacc[rb][m + 3], alpha, scr_addr);
+                agpr_scale_via_lds(oacc[rb][16], alpha, scr_addr);
             }
         }
     };

@@ -175,4 +175,50 @@ struct DmaLane {
     unsigned kb2[4];     // kFast: 4 q k_ss, q = 0..3 (K blocks: rows 4 (i & 3) + q)
 };
 
+// acc *= alpha for MFMA accumulators, through LDS (16 bytes per lane and accumulator, 1 KiB
+// apart from `lds_addr`): the accumulators are read and written only by asm with AGPR operands.
+// Four at a time: two LDS round trips per four accumulators.
+__device__ __forceinline__ void agpr_scale4_via_lds(float4_t& a0, float4_t& a1, float4_t& a2, float4_t& a3,
+                                                    float alpha, unsigned lds_addr) {
+    float4_t t0, t1, t2, t3;
+    asm volatile(
+        "ds_write_b128 %4, %5\n\tds_write_b128 %4, %6 offset:1024\n\t"
+        "ds_write_b128 %4, %7 offset:2048\n\tds_write_b128 %4, %8 offset:3072\n\t"
+        "s_waitcnt lgkmcnt(0)\n\t"
+        "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:1024\n\t"
+        "ds_read_b128 %2, %4 offset:2048\n\tds_read_b128 %3, %4 offset:3072\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+        : "v"(lds_addr), "a"(a0), "a"(a1), "a"(a2), "a"(a3)
+        : "memory");
+    t0 *= alpha;
+    t1 *= alpha;
+    t2 *= alpha;
+    t3 *= alpha;
+    asm volatile(
+        "ds_write_b128 %4, %5\n\tds_write_b128 %4, %6 offset:1024\n\t"
+        "ds_write_b128 %4, %7 offset:2048\n\tds_write_b128 %4, %8 offset:3072\n\t"
+        "s_waitcnt lgkmcnt(0)\n\t"
+        "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:1024\n\t"
+        "ds_read_b128 %2, %4 offset:2048\n\tds_read_b128 %3, %4 offset:3072\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&a"(a0), "=&a"(a1), "=&a"(a2), "=&a"(a3)
+        : "v"(lds_addr), "v"(t0), "v"(t1), "v"(t2), "v"(t3)
+        : "memory");
+}
+
+// The same for one accumulator.
+__device__ __forceinline__ void agpr_scale_via_lds(float4_t& acc, float alpha, unsigned lds_addr) {
+    float4_t t;
+    asm volatile("ds_write_b128 %1, %2\n\ts_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+                 : "=v"(t)
+                 : "v"(lds_addr), "a"(acc)
+                 : "memory");
+    t *= alpha;
+    asm volatile("ds_write_b128 %1, %2\n\ts_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+                 : "=a"(acc)
+                 : "v"(lds_addr), "v"(t)
+                 : "memory");
+}
+
 }  // namespace pd
