@@ -1,0 +1,151 @@
+"""Seeded random sweep of both operators against the float64 oracle.
+
+The hand-picked cases of test_decode_gpu.py and test_prefill_gpu.py each vary one or two things
+at a time. Here every case draws all of them at once, so combinations that no single test
+fixes are exercised too:
+- GQA group sizes with qmax * G <= 48;
+- batches of 1-6 sequences, with contexts from 0 to ~6,000 keys and padding slots;
+- block sizes 1, 8, 16, 32, 48, 64 and 1584 (the reference's), in HND and NHD physical order;
+- sliding windows, non-causal rows, NaN-poisoned freed pages and outlier rows;
+- strided queries, and split counts from 1 to 128.
+
+Prefill cases draw group sizes, batches, chunk lengths, block sizes, layouts and chunk offsets
+(rows before the first key, chunks ending the sequence or past it).
+
+Tolerance, on the rows that the reference writes:
+- Prefill (fp32 output): max-abs <= 2e-3 and mean-abs <= 2e-4. Rows that see no key must be 0.
+- Decode (fp16 output): the same bar, applied to the value before its rounding to fp16
+  (workload.fp16_output_errors, pinned by tests/test_checker.py). Outlier rows in short contexts
+  give outputs in the hundreds, where fp16's own spacing is 0.125-0.25, so no fp16 result can be
+  within 2e-3 there. A correctly rounded answer fp16(ref) scores the same as the kernel on such
+  a case: max-abs 6.24e-2 against 6.26e-2, mean-abs 1.971e-4 against 1.975e-4.
+
+Each case prints its parameters before it runs.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import workload as kvc
+from mi50_vllm_lab_amd import pth_dec
+from oracle import attention as orc
+
+pytestmark = pytest.mark.gpu
+
+NSEG = 128
+N_DECODE = 24
+N_PREFILL = 12
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def context_length(rng, hi):
+    """An integer in [0, hi): log-uniform or uniform with equal odds, so that very short and
+    multi-thousand-key contexts are both common."""
+    if rng.random() < 0.5:
+        return int(math.exp(rng.uniform(0.0, math.log(hi + 1.0)))) - 1
+    return int(rng.integers(0, hi))
+
+
+def draw_decode(i):
+    rng = np.random.default_rng(9100 + i)
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    qmax = int(rng.integers(1, 9))
+    G = int(rng.integers(1, min(48 // qmax, 12) + 1))
+    nseq = int(rng.integers(1, 7))
+    ctxs = [context_length(rng, 6000) for _ in range(nseq)]
+    qlens = [int(rng.integers(1, qmax + 1)) for _ in range(nseq)]
+    qlens[0] = qmax
+    if nseq > 1 and rng.random() < 0.25:
+        ctxs[-1], qlens[-1] = 0, 0  # a padded slot
+    window = -1 if rng.random() < 0.5 else int(rng.integers(1, 3000))
+    return dict(
+        ctxs=ctxs, qlens=qlens, hq=G * hkv, hkv=hkv, qmax=qmax,
+        bs=int(rng.choice([1, 8, 16, 32, 48, 64, 1584])),
+        layout=str(rng.choice(["HND", "NHD"])),
+        window=window,
+        causal=bool(rng.random() < 0.7),
+        poison=bool(window > 0 and rng.random() < 0.5),
+        kv_mode=str(rng.choice(["normal", "uniform"])),
+        outlier=0.01 if rng.random() < 0.2 else 0.0,
+        q_noncontig=bool(rng.random() < 0.3),
+        nsplit=int(rng.integers(1, NSEG + 1)),
+        seed=9100 + i,
+    )
+
+
+@pytest.mark.parametrize("i", range(N_DECODE))
+def test_decode_random(i):
+    p = draw_decode(i)
+    say(f"decode sweep {i}: {p}")
+    c = kvc.make_case(p["ctxs"], p["qlens"], num_q_heads=p["hq"], num_kv_heads=p["hkv"], block_size=p["bs"],
+                      layout=p["layout"], seed=p["seed"], kv_mode=p["kv_mode"], outlier_frac=p["outlier"],
+                      q_noncontig=p["q_noncontig"], window=p["window"], causal=p["causal"], poison=p["poison"])
+    ref, written = orc.paged_decode(c.q, c.cache.key_cache, c.cache.value_cache, c.cache.k_scale, c.cache.v_scale,
+                                    c.block_table, c.seq_lens, c.query_start_loc, c.num_seqs, c.scale, c.window,
+                                    c.causal, p["qmax"])
+    d = c.to("cuda")
+    T = d.num_tokens
+    out = torch.full((T, p["hq"], 256), float("nan"), dtype=torch.float16, device="cuda")
+    po, pm, pl = kvc.partial_buffers(max(T, 1), p["hq"], NSEG, "cuda")
+    pth_dec.decode(d.q, d.cache.key_cache, d.cache.value_cache, d.cache.k_scale, d.cache.v_scale, d.block_table,
+                   d.seq_lens, d.query_start_loc, out, d.scale, po, pm, pl, d.num_seqs, p["qmax"], p["nsplit"],
+                   d.window, d.causal)
+    torch.cuda.synchronize()
+    o = out.double().cpu().numpy()
+    assert np.isfinite(o[written]).all()
+    emax, emean, excess, mean_excess = kvc.fp16_output_errors(o[written], ref[written])
+    say(f"  max-abs {emax:.2e} mean-abs {emean:.2e}; beyond the fp16 rounding: {excess:.2e} (<= 0), "
+        f"mean {mean_excess:.2e} (<= 2e-4)")
+    assert excess <= 0.0 and mean_excess <= 2e-4, (i, emax, emean, excess, mean_excess)
+
+
+def draw_prefill(i):
+    rng = np.random.default_rng(9300 + i)
+    hkv = int(rng.choice([1, 2, 4]))
+    G = int(rng.integers(1, 9))
+    nseq = int(rng.integers(1, 4))
+    sq = int(rng.integers(1, 129))
+    ctxs = [context_length(rng, 2000) for _ in range(nseq)]
+    q_abs = []
+    for c in ctxs:
+        r = rng.random()
+        if r < 0.5:
+            q_abs.append(c)  # the chunk ends the sequence
+        elif r < 0.75:
+            q_abs.append(int(rng.integers(-sq, c + 1)))  # rows before the first key or mid-sequence
+        else:
+            q_abs.append(c + sq + int(rng.integers(0, 50)))  # past the end: every row sees every key
+    return dict(ctxs=ctxs, sq=sq, q_abs=q_abs, hq=G * hkv, hkv=hkv,
+                bs=int(rng.choice([1, 8, 16, 32, 48, 1584])), layout=str(rng.choice(["HND", "NHD"])),
+                kv_mode=str(rng.choice(["normal", "uniform"])), seed=9300 + i)
+
+
+@pytest.mark.parametrize("i", range(N_PREFILL))
+def test_prefill_random(i):
+    p = draw_prefill(i)
+    say(f"prefill sweep {i}: {p}")
+    c = kvc.make_case(p["ctxs"], [p["sq"]] * len(p["ctxs"]), num_q_heads=p["hq"], num_kv_heads=p["hkv"],
+                      block_size=p["bs"], layout=p["layout"], seed=p["seed"], kv_mode=p["kv_mode"])
+    ref, written = orc.paged_prefill(kvc.prefill_query(c), c.cache.key_cache, c.cache.value_cache, c.cache.k_scale,
+                                     c.cache.v_scale, c.block_table, c.seq_lens, c.scale,
+                                     torch.tensor(p["q_abs"]), None)
+    d = c.to("cuda")
+    q = kvc.prefill_query(d)
+    out = torch.full((q.shape[0], q.shape[2], q.shape[1], 256), float("nan"), dtype=torch.float32, device="cuda")
+    pth_dec.forward_pth(q, d.cache.key_cache, d.cache.value_cache, d.block_table, d.seq_lens, d.scale,
+                        torch.tensor(p["q_abs"], dtype=torch.int32, device="cuda"), out=out)
+    torch.cuda.synchronize()
+    o = out.double().cpu().numpy()
+    assert np.isfinite(o).all()
+    assert (o[~written] == 0).all()  # rows that see no key are written as 0
+    e = np.abs(o[written] - ref[written])
+    emax, emean = (float(e.max()), float(e.mean())) if e.size else (0.0, 0.0)
+    say(f"  max-abs {emax:.2e} mean-abs {emean:.2e}")
+    assert emax <= 2e-3 and emean <= 2e-4, (i, emax, emean)

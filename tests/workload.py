@@ -252,3 +252,35 @@ def prefill_flops(seq_lens, q_abs, sq: int, num_q_heads: int) -> int:
         for i in range(sq):
             total += max(0, min(int(seq), int(qa) + i + 1))
     return 4 * HEAD_DIM * num_q_heads * total
+
+
+def fp16_half_ulp(x):
+    """Half the spacing of fp16 numbers at |x| (numpy, elementwise): the rounding error of a
+    correctly rounded fp16 result (2^-25 below the normal range)."""
+    import numpy as np
+    a = np.maximum(np.abs(np.asarray(x, dtype=np.float64)), 2.0 ** -14)
+    return 0.5 * np.exp2(np.floor(np.log2(a)) - 10)
+
+
+def fp16_output_errors(out, ref, tol_max=2e-3, tol_mean=2e-4):
+    """Errors of an fp16 output against the float64 oracle, with the tolerance applied to the
+    value computed before the final rounding to fp16.
+
+    An fp16 result of magnitude >= 8 cannot be within 2e-3 of the exact answer: its spacing there
+    is 2^-7. So element by element |out - ref| may exceed tol_max by half an fp16 spacing at that
+    magnitude, taking the larger of |out| and |ref|, which covers a rounding across a power of two.
+    The mean-abs error may exceed that of the correctly rounded answer fp16(ref) by tol_mean.
+    Below |ref| = 1 the allowance is at most 2^-12 (2.4e-4).
+
+    Returns (max-abs, mean-abs, worst excess over the element bound, mean-abs excess over fp16(ref)).
+    The output passes when both excesses are <= 0 and tol_mean respectively.
+    """
+    import numpy as np
+    o = np.asarray(out, dtype=np.float64)
+    r = np.asarray(ref, dtype=np.float64)
+    if o.size == 0:
+        return 0.0, 0.0, -tol_max, 0.0
+    e = np.abs(o - r)
+    bound = tol_max + fp16_half_ulp(np.maximum(np.abs(o), np.abs(r)))
+    r16 = r.astype(np.float16).astype(np.float64)
+    return float(e.max()), float(e.mean()), float((e - bound).max()), float(e.mean() - np.abs(r16 - r).mean())
