@@ -28,8 +28,9 @@
 //
 // Per 32-key tile, per wave
 //   S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims of K (int8 widened to fp16
-//     exactly: 0x6400|(b^0x80) encodes 1024+b+128), B = Q^T held in registers; the four
-//     accumulation chains (2 key blocks x 2 row blocks) are interleaved.
+//     exactly by SDWA byte conversions, with no bias, so the fp32 accumulators only ever hold
+//     partial scores), B = Q^T held in registers; the four accumulation chains (2 key blocks x
+//     2 row blocks) are interleaved.
 //   softmax: base 2, fp32, online. A row's running max is raised only when a tile exceeds it
 //     by > 2^4: each lane tests its own 8 scores and one ballot decides; only then is the row
 //     max reduced across lanes and O rescaled (rare after the first tile). P' = p * v_scale * 16
@@ -235,7 +236,6 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     // ---- Q^T operand (B of S^T = K Q^T) of every row block; lane (lg, li) holds row 16 rb + li,
     //      dims 64 (st / 2) + 16 lg + 8 (st % 2) + [0, 8) in qop[rb][st] ----
     half8_t qop[NRB][8];
-    float4_t qneg[NRB];  // -1152 sum_d q_d of the row (every element): the widening bias of K
     bool rvalid[NRB];
     int rpos[NRB];
 #pragma unroll
@@ -401,16 +401,6 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         }
         __syncthreads();
     }
-    {
-        const half8_t nb = (half8_t)(_Float16)(-kWidenBias);
-#pragma unroll
-        for (int rb = 0; rb < NRB; ++rb) {
-            float4_t acc = (float4_t)0.f;
-#pragma unroll
-            for (int st = 0; st < 8; ++st) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(nb, qop[rb][st], acc, 0, 0, 0);
-            qneg[rb] = acc;
-        }
-    }
 
     // ---- per-lane LDS read offsets inside a slot ----
     // K operand (u, c): row 16 u + li, source chunk 4 c + lg
@@ -445,8 +435,8 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
 
     int tile_cur = tb;  // the tile being computed
 
-    // ---- S^T = K Q^T for every row block (the accumulator starts at -1152 sum q, the widening
-    //      bias of K), times k_scale, relative to the running max: sv = s - m (log2 units; s itself
+    // ---- S^T = K Q^T for every row block (K exact in fp16, the widening bias removed before the
+    //      products), times k_scale, relative to the running max: sv = s - m (log2 units; s itself
     //      while a row has no max yet); masked scores are -inf. Returns whether some row has to
     //      raise its max: its tile max exceeds the running max by more than kLazy, or it has none ----
     auto tile_scores = [&](const TileOps& o, float (&sv)[NRB][8], bool& interior) __attribute__((always_inline)) {
@@ -458,11 +448,14 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
             for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
-                    const half8_t kf = hh == 0 ? widen_i8x8(kr[u].x, kr[u].y) : widen_i8x8(kr[u].z, kr[u].w);
+                    // K exact in fp16 (no widening bias): the accumulator holds only partial
+                    // scores, whose rounding is ~1152 / |k| times smaller than with the bias
+                    // removed at the end
+                    const half8_t kf = hh == 0 ? widen_i8x8_exact(kr[u].x, kr[u].y) : widen_i8x8_exact(kr[u].z, kr[u].w);
 #pragma unroll
                     for (int rb = 0; rb < NRB; ++rb)
                         sacc[rb][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            kf, qop[rb][2 * c + hh], (c | hh) ? sacc[rb][u] : qneg[rb], 0, 0, 0);
+                            kf, qop[rb][2 * c + hh], (c | hh) ? sacc[rb][u] : (float4_t)0.f, 0, 0, 0);
                 }
             }
         }
