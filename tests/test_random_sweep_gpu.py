@@ -8,6 +8,8 @@ fixes are exercised too:
 - block sizes 1, 8, 16, 32, 48, 64 and 1584 (the reference's), in HND and NHD physical order;
 - sliding windows, non-causal rows, NaN-poisoned freed pages and outlier rows;
 - strided queries, and split counts from 1 to 128.
+Every output and partial buffer has sentinel guards on both sides that must stay untouched, and
+the inputs must be unchanged afterwards.
 
 Prefill cases draw group sizes, batches, chunk lengths, block sizes, layouts and chunk offsets
 (rows before the first key, chunks ending the sequence or past it).
@@ -36,13 +38,35 @@ from oracle import attention as orc
 pytestmark = pytest.mark.gpu
 
 NSEG = 128
-N_DECODE = 24
-N_PREFILL = 12
+N_DECODE = 64
+N_PREFILL = 32
 
 
 def say(msg):
     print(msg, flush=True)
     sys.stdout.flush()
+
+
+GUARD = 1 << 14  # elements of sentinel on each side of every output and partial buffer
+SENTINEL = 12345.0
+
+
+def guarded(shape, dtype, fill):
+    """A device buffer of `shape` with GUARD sentinel elements on each side: (whole, body)."""
+    n = int(np.prod(shape))
+    whole = torch.full((n + 2 * GUARD,), SENTINEL, dtype=dtype, device="cuda")
+    body = whole[GUARD:GUARD + n].view(shape)
+    body.fill_(fill)
+    return whole, body
+
+
+def guards_intact(whole):
+    return bool((whole[:GUARD] == SENTINEL).all()) and bool((whole[-GUARD:] == SENTINEL).all())
+
+
+def fingerprint(*tensors):
+    """Exact integer checksums of the operator's inputs (which it must not write)."""
+    return [int(x.contiguous().view(torch.uint8).long().sum()) for x in tensors]
 
 
 def context_length(rng, hi):
@@ -92,12 +116,18 @@ def test_decode_random(i):
                                     c.causal, p["qmax"])
     d = c.to("cuda")
     T = d.num_tokens
-    out = torch.full((T, p["hq"], 256), float("nan"), dtype=torch.float16, device="cuda")
-    po, pm, pl = kvc.partial_buffers(max(T, 1), p["hq"], NSEG, "cuda")
+    inputs = (d.q, d.cache.kv, d.block_table, d.seq_lens, d.query_start_loc)
+    before = fingerprint(*inputs)
+    wo, out = guarded((T, p["hq"], 256), torch.float16, float("nan"))
+    wpo, po = guarded((max(T, 1), p["hq"], NSEG, 256), torch.float32, 0.0)
+    wpm, pm = guarded((max(T, 1), p["hq"], NSEG), torch.float32, 0.0)
+    wpl, pl = guarded((max(T, 1), p["hq"], NSEG), torch.float32, 0.0)
     pth_dec.decode(d.q, d.cache.key_cache, d.cache.value_cache, d.cache.k_scale, d.cache.v_scale, d.block_table,
                    d.seq_lens, d.query_start_loc, out, d.scale, po, pm, pl, d.num_seqs, p["qmax"], p["nsplit"],
                    d.window, d.causal)
     torch.cuda.synchronize()
+    assert all(guards_intact(x) for x in (wo, wpo, wpm, wpl)), "a write outside the output or partial buffers"
+    assert fingerprint(*inputs) == before, "an input was written"
     o = out.double().cpu().numpy()
     assert np.isfinite(o[written]).all()
     emax, emean, excess, mean_excess = kvc.fp16_output_errors(o[written], ref[written])
@@ -138,13 +168,19 @@ def test_prefill_random(i):
                                      torch.tensor(p["q_abs"]), None)
     d = c.to("cuda")
     q = kvc.prefill_query(d)
-    out = torch.full((q.shape[0], q.shape[2], q.shape[1], 256), float("nan"), dtype=torch.float32, device="cuda")
+    inputs = (q, d.cache.kv, d.block_table, d.seq_lens)
+    before = fingerprint(*inputs)
+    wo, out = guarded((q.shape[0], q.shape[2], q.shape[1], 256), torch.float32, float("nan"))
     pth_dec.forward_pth(q, d.cache.key_cache, d.cache.value_cache, d.block_table, d.seq_lens, d.scale,
                         torch.tensor(p["q_abs"], dtype=torch.int32, device="cuda"), out=out)
     torch.cuda.synchronize()
+    assert guards_intact(wo), "a write outside the output"
+    assert fingerprint(*inputs) == before, "an input was written"
     o = out.double().cpu().numpy()
-    assert np.isfinite(o).all()
-    assert (o[~written] == 0).all()  # rows that see no key are written as 0
+    bad = np.argwhere(~np.isfinite(o))
+    assert bad.size == 0, f"non-finite outputs at (seq, token, head, dim) {bad[:8].tolist()}"
+    nz = np.argwhere((o != 0) & ~written[..., None, None])
+    assert nz.size == 0, f"rows that see no key must be 0: {nz[:8].tolist()}"
     e = np.abs(o[written] - ref[written])
     emax, emean = (float(e.max()), float(e.mean())) if e.size else (0.0, 0.0)
     say(f"  max-abs {emax:.2e} mean-abs {emean:.2e}")
