@@ -473,24 +473,23 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         for (int rb = 0; rb < NRB; ++rb) {
             const bool fresh = m_run[rb] == kNegInf;
             const float nm = fresh ? 0.f : -m_run[rb];
-            float mx = kNegInf;
-            if (interior) {
+            // the scores are formed in place in both cases (no copies where the paths meet); a tile
+            // at the edge of the visible range then masks its invisible keys to -inf
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    sv[rb][e] = __builtin_fmaf(sacc[rb][e >> 2][e & 3], ks[e], nm);
-                    mx = fmaxf(mx, sv[rb][e]);
-                }
-            } else {
+            for (int e = 0; e < 8; ++e) sv[rb][e] = __builtin_fmaf(sacc[rb][e >> 2][e & 3], ks[e], nm);
+            if (!interior) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int t = kb + 16 * (e >> 2) + 4 * lg + (e & 3);
                     const int rp = rpos[rb];
                     const bool vis = rvalid[rb] & (t >= lo) & (t < hi) & (!a.causal | (t <= rp)) &
                                      ((a.window <= 0) | ((rp - t) < a.window));
-                    sv[rb][e] = vis ? __builtin_fmaf(sacc[rb][e >> 2][e & 3], ks[e], nm) : kNegInf;
-                    mx = fmaxf(mx, sv[rb][e]);
+                    sv[rb][e] = vis ? sv[rb][e] : kNegInf;
                 }
             }
+            float mx = kNegInf;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, sv[rb][e]);
             need |= fresh ? mx > kNegInf : mx > kLazy;
         }
         return need;
