@@ -12,7 +12,10 @@ Every output and partial buffer has sentinel guards on both sides that must stay
 the inputs must be unchanged afterwards.
 
 Prefill cases draw group sizes, batches, chunk lengths, block sizes, layouts and chunk offsets
-(rows before the first key, chunks ending the sequence or past it).
+(rows before the first key, chunks ending the sequence or past it). KV-cache writer cases draw
+token and head counts, block sizes, layouts, dtypes, padding slots and row magnitudes over many
+decades, with key and value as strided views into one fused QKV buffer (vLLM's form), and must
+match the oracle's cache bytes exactly.
 
 Tolerance, on the rows that the reference writes:
 - Prefill (fp32 output): max-abs <= 2e-3 and mean-abs <= 2e-4. Rows that see no key must be 0.
@@ -185,3 +188,47 @@ def test_prefill_random(i):
     emax, emean = (float(e.max()), float(e.mean())) if e.size else (0.0, 0.0)
     say(f"  max-abs {emax:.2e} mean-abs {emean:.2e}")
     assert emax <= 2e-3 and emean <= 2e-4, (i, emax, emean)
+
+
+N_WRITE = 16
+
+
+def draw_write(i):
+    rng = np.random.default_rng(9500 + i)
+    dtype = [torch.float16, torch.bfloat16, torch.float32][int(rng.integers(0, 3))]
+    # row magnitudes over many decades, inside each dtype's normal range
+    lo_exp, hi_exp = {torch.float16: (-3, 3), torch.bfloat16: (-20, 20), torch.float32: (-20, 20)}[dtype]
+    return dict(T=int(rng.integers(1, 3000)), hkv=int(rng.choice([1, 2, 4, 8])), hq=int(rng.choice([8, 24, 32])),
+                bs=int(rng.choice([1, 8, 16, 32, 48, 1584])), layout=str(rng.choice(["HND", "NHD"])), dtype=dtype,
+                lo_exp=lo_exp, hi_exp=hi_exp, pad=float(rng.choice([0.0, 0.1, 0.5])), seed=9500 + i)
+
+
+@pytest.mark.parametrize("i", range(N_WRITE))
+def test_cache_write_random(i):
+    """The KV-cache writer on key/value as vLLM hands them over: strided views into one fused
+    QKV projection output [T, (Hq + 2 Hkv) x 256]. Cache bytes must equal the oracle's bit for
+    bit, and the rows of padding slots (-1) and of unused slots must stay as they were."""
+    from oracle import kvwrite as kvw
+    p = draw_write(i)
+    say(f"cache write sweep {i}: {p}")
+    T, hkv, hq, bs = p["T"], p["hkv"], p["hq"], p["bs"]
+    g = torch.Generator().manual_seed(p["seed"])
+    qkv = torch.randn((T, (hq + 2 * hkv) * 256), generator=g)
+    mag = torch.exp(torch.empty((T, 1)).uniform_(p["lo_exp"] * math.log(10), p["hi_exp"] * math.log(10), generator=g))
+    qkv = (qkv * mag).to(p["dtype"])
+    nblk = (T + bs - 1) // bs + 2
+    slots = torch.randperm(nblk * bs, generator=g)[:T].to(torch.int64)
+    slots[torch.rand(T, generator=g) < p["pad"]] = -1
+    ref = kvc.allocate_cache(nblk, bs, hkv, p["layout"])
+    ref.kv.copy_(torch.randint(-128, 128, ref.kv.shape, dtype=torch.int8, generator=g))
+    dev = kvc.clone_cache(ref, "cuda")
+    k_cpu = qkv[:, hq * 256:(hq + hkv) * 256].reshape(T, hkv, 256)
+    v_cpu = qkv[:, (hq + hkv) * 256:].reshape(T, hkv, 256)
+    kvw.write_rows(k_cpu.float(), v_cpu.float(), ref.key_cache, ref.value_cache, ref.k_scale, ref.v_scale, slots)
+    qkv_d = qkv.cuda()
+    k = qkv_d[:, hq * 256:(hq + hkv) * 256].view(T, hkv, 256)
+    v = qkv_d[:, (hq + hkv) * 256:].view(T, hkv, 256)
+    assert not k.is_contiguous() and k.stride(0) == (hq + 2 * hkv) * 256
+    pth_dec.cache_write(k, v, dev.key_cache, dev.value_cache, dev.k_scale, dev.v_scale, slots.cuda())
+    torch.cuda.synchronize()
+    assert torch.equal(dev.kv.cpu(), ref.kv)
