@@ -156,6 +156,19 @@ int pth_fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_tens
                    int errlen);
 
 /*
+ * No counterpart in the reference. pth_fa_forward with the decode's numerics: K converted to
+ * fp16 without the widening bias, so the fp32 score accumulators hold only partial scores, and
+ * P' carried as fp16 hi + lo (~22 bits instead of 11). It is for callers whose caches hold rows
+ * with very large scales (attention sinks, outlier tokens), where pth_fa_forward's single-fp16
+ * P' can miss max-abs 2e-3. It is slower: the P.V products double. Arguments, checks, errors and
+ * return codes are those of pth_fa_forward.
+ */
+int pth_fa_forward_exact(const pd_tensor* q, const pd_tensor* key_cache, const pd_tensor* value_cache,
+                         const pd_tensor* block_table, const pd_tensor* seq_lens, double scale,
+                         const pd_tensor* q_abs_offset, const pd_tensor* out, hipStream_t stream, char* err,
+                         int errlen);
+
+/*
  * KV-cache writer and quantiser: the producer of the 520-byte rows the two operators read.
  * Replaces vLLM's cache update for int8 per-token-head KV, which the reference calls as
  * do_kv_cache_update(layer, key, value, kv_cache, slot_mapping)

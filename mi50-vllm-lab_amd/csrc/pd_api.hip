@@ -245,9 +245,10 @@ int pth_dec_decode(const pd_tensor* q, const pd_tensor* key_cache, const pd_tens
     return 0;
 }
 
-int pth_fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_tensor* value_cache,
-                   const pd_tensor* block_table, const pd_tensor* seq_lens, double scale, const pd_tensor* q_abs_offset,
-                   const pd_tensor* out, hipStream_t stream, char* err, int errlen) {
+static int fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_tensor* value_cache,
+                      const pd_tensor* block_table, const pd_tensor* seq_lens, double scale,
+                      const pd_tensor* q_abs_offset, const pd_tensor* out, hipStream_t stream, char* err, int errlen,
+                      bool exact) {
     if (!q || !key_cache || !value_cache || !block_table || !seq_lens || !q_abs_offset || !out)
         return fail(err, errlen, "null tensor descriptor");
     if (!(q->dtype == PD_DTYPE_FP32 && q->ndim == 4 && is_contig(q)))
@@ -319,7 +320,7 @@ int pth_fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_tens
     const int64_t span = (key_cache->sizes[0] - 1) * key_cache->strides[0] + (bs - 1) * key_cache->strides[1] +
                          (Hkv - 1) * key_cache->strides[2] + 8;
     p.bt32 = span < ((int64_t)1 << 35);
-    const hipError_t e = launch_prefill(p, (int)B, (int)Hkv, stream);
+    const hipError_t e = launch_prefill(p, (int)B, (int)Hkv, stream, exact);
     if (e != hipSuccess) {
         char msg[256];
         snprintf(msg, sizeof msg, "pth_fa launch failed: %s", hipGetErrorString(e));
@@ -327,6 +328,21 @@ int pth_fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_tens
         return 2;
     }
     return 0;
+}
+
+int pth_fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_tensor* value_cache,
+                   const pd_tensor* block_table, const pd_tensor* seq_lens, double scale, const pd_tensor* q_abs_offset,
+                   const pd_tensor* out, hipStream_t stream, char* err, int errlen) {
+    return fa_forward(q, key_cache, value_cache, block_table, seq_lens, scale, q_abs_offset, out, stream, err, errlen,
+                      false);
+}
+
+int pth_fa_forward_exact(const pd_tensor* q, const pd_tensor* key_cache, const pd_tensor* value_cache,
+                         const pd_tensor* block_table, const pd_tensor* seq_lens, double scale,
+                         const pd_tensor* q_abs_offset, const pd_tensor* out, hipStream_t stream, char* err,
+                         int errlen) {
+    return fa_forward(q, key_cache, value_cache, block_table, seq_lens, scale, q_abs_offset, out, stream, err, errlen,
+                      true);
 }
 
 int pth_cache_write(const pd_tensor* key, const pd_tensor* value, const pd_tensor* key_cache,

@@ -125,7 +125,8 @@ constexpr size_t kScratchBytes = size_t(32) << 20;
 hipError_t scratch_address(void** out);
 
 // chunked prefill (pd_prefill.hip)
-hipError_t launch_prefill(const FaParams& p, int batch, int heads_kv, hipStream_t stream);
+// exact: K converted to fp16 without the widening bias and P' as fp16 hi + lo (pth_fa_forward_exact)
+hipError_t launch_prefill(const FaParams& p, int batch, int heads_kv, hipStream_t stream, bool exact);
 
 // cache writer (pd_cache_write.hip); dtype is a PD_DTYPE_* code of key and value
 hipError_t launch_cache_write(const CacheWriteParams& p, int dtype, hipStream_t stream);

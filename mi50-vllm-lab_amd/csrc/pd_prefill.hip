@@ -73,7 +73,7 @@ __device__ __forceinline__ void wait_quarters(int later, bool tail) {
     }
 }
 
-template <bool kFast>
+template <bool kFast, bool kExact>
 __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaParams a) {
     constexpr int kLdsRaw = 0;
     constexpr int kLdsH = kLdsRaw + kFaRaw * kSlot;
@@ -261,7 +261,11 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
         lds_u8* H = hbuf(n);
         if (j < 4) {
             const int u = j >> 1, hh = j & 1;
-            const half8_t kf = hh == 0 ? widen_i8x8(r.kr[u].x, r.kr[u].y) : widen_i8x8(r.kr[u].z, r.kr[u].w);
+            half8_t kf;
+            if constexpr (kExact)
+                kf = hh == 0 ? widen_i8x8_exact(r.kr[u].x, r.kr[u].y) : widen_i8x8_exact(r.kr[u].z, r.kr[u].w);
+            else
+                kf = hh == 0 ? widen_i8x8(r.kr[u].x, r.kr[u].y) : widen_i8x8(r.kr[u].z, r.kr[u].w);
             *(lds_half8*)(H + ((2 * w + hh) * 2 + u) * 1024 + 16 * l) = kf;
         } else if (j < 8) {
             *(lds_half8*)(H + kFaHK + (w + 4 * (j - 4)) * 1024 + 16 * l) =
@@ -319,7 +323,7 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
 #pragma unroll
                 for (int rb = 0; rb < kFaRB; ++rb)
                     sacc[rb][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[st & 1][u], qop[rb][st],
-                                                                         st ? sacc[rb][u] : (float4_t)qneg[rb], 0, 0, 0);
+                                                                         st ? sacc[rb][u] : (float4_t)(kExact ? 0.f : qneg[rb]), 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
         const int kb = n * kTile;
@@ -392,7 +396,7 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
         half8_t vf[17];
 #pragma unroll
         for (int m = 0; m < kVAhead; ++m) vf[m] = *(const lds_half8*)(H + m * 1024);
-        half8_t pop[kFaRB];
+        half8_t pop[kFaRB], plo[kFaRB];
 #pragma unroll
         for (int rb = 0; rb < kFaRB; ++rb) {
             float psum = 0.f;
@@ -400,7 +404,9 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
             for (int e = 0; e < 8; ++e) {
                 const float p = __builtin_amdgcn_exp2f(sv[rb][e]);
                 psum += p;
-                pop[rb][e] = (_Float16)(p * vs[e]);
+                const _Float16 h = (_Float16)(p * vs[e]);
+                pop[rb][e] = h;
+                if constexpr (kExact) plo[rb][e] = (_Float16)__builtin_fmaf(p, vs[e], -(float)h);
             }
             l_run[rb] += psum;
         }
@@ -411,6 +417,11 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
 #pragma unroll
             for (int rb = 0; rb < kFaRB; ++rb)
                 oacc[rb][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[m], pop[rb], oacc[rb][m], 0, 0, 0);
+            if constexpr (kExact) {
+#pragma unroll
+                for (int rb = 0; rb < kFaRB; ++rb)
+                    oacc[rb][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[m], plo[rb], oacc[rb][m], 0, 0, 0);
+            }
             if (m >= 2 && m < 12) widen_store(n + 1, wr, m - 2);
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -515,12 +526,18 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
 // ---------------------------------------------------------------------------------------
 // host side
 
-hipError_t launch_prefill(const FaParams& p, int batch, int heads_kv, hipStream_t stream) {
+hipError_t launch_prefill(const FaParams& p, int batch, int heads_kv, hipStream_t stream, bool exact) {
     const dim3 grid((p.Sq + p.tok_per_wg - 1) / p.tok_per_wg, heads_kv, batch);
-    if (fast_block_table(p.block_size, p.k_ss))
-        hipLaunchKernelGGL((pd_prefill_kernel<true>), grid, dim3(kFaWaves * 64), 0, stream, p);
+    const dim3 block(kFaWaves * 64);
+    const bool fast = fast_block_table(p.block_size, p.k_ss);
+    if (fast && !exact)
+        hipLaunchKernelGGL((pd_prefill_kernel<true, false>), grid, block, 0, stream, p);
+    else if (!exact)
+        hipLaunchKernelGGL((pd_prefill_kernel<false, false>), grid, block, 0, stream, p);
+    else if (fast)
+        hipLaunchKernelGGL((pd_prefill_kernel<true, true>), grid, block, 0, stream, p);
     else
-        hipLaunchKernelGGL((pd_prefill_kernel<false>), grid, dim3(kFaWaves * 64), 0, stream, p);
+        hipLaunchKernelGGL((pd_prefill_kernel<false, true>), grid, block, 0, stream, p);
     return hipGetLastError();
 }
 

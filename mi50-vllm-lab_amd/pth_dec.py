@@ -49,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "pth_dec_decode",
     "pth_dec_version",
     "pth_fa_forward",
+    "pth_fa_forward_exact",
     "pth_cache_write",
 )
 
@@ -105,6 +106,8 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.pth_dec_decode.restype = c_int
     lib.pth_fa_forward.argtypes = [tp] * 5 + [c_double, tp, tp, vp, ctypes.c_char_p, c_int]
     lib.pth_fa_forward.restype = c_int
+    lib.pth_fa_forward_exact.argtypes = lib.pth_fa_forward.argtypes
+    lib.pth_fa_forward_exact.restype = c_int
     lib.pth_cache_write.argtypes = [tp] * 7 + [vp, ctypes.c_char_p, c_int]
     lib.pth_cache_write.restype = c_int
     lib.pth_dec_version.argtypes = []
@@ -168,12 +171,15 @@ def decode(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, 
 
 def forward_pth(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, block_table: torch.Tensor,
                 seq_lens: torch.Tensor, scale: float, q_abs_offset: torch.Tensor,
-                out: torch.Tensor | None = None) -> torch.Tensor:
+                out: torch.Tensor | None = None, exact: bool = False) -> torch.Tensor:
     """Causal chunked prefill over the int8 per-token-head cache; returns fp32 [B, Sq, Hq, 256].
 
     q: fp32 [B, Hq, Sq, 256] contiguous; query token i of sequence b is at absolute position
     q_abs_offset[b] + i and attends to keys k <= that position, k < seq_lens[b].
     Reference: kernels/fa_pth/pth_fa.cpp:41-85 (same arguments; `out` may be passed in).
+    exact=True runs pth_fa_forward_exact, which has no counterpart in the reference: K without
+    the widening bias and P' as fp16 hi + lo, for caches with very large scales (outlier
+    tokens), at about twice the P.V matrix work.
     """
     if not q.is_cuda:
         raise RuntimeError("q must be contiguous fp32 [B, Hq, Sq, D]")
@@ -185,8 +191,9 @@ def forward_pth(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Ten
     err = ctypes.create_string_buffer(256)
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
-        rc = lib.pth_fa_forward(*[ctypes.byref(x) for x in descs], float(scale), ctypes.byref(qa), ctypes.byref(od),
-                                ctypes.c_void_p(stream), err, len(err))
+        fn = lib.pth_fa_forward_exact if exact else lib.pth_fa_forward
+        rc = fn(*[ctypes.byref(x) for x in descs], float(scale), ctypes.byref(qa), ctypes.byref(od),
+                ctypes.c_void_p(stream), err, len(err))
     if rc != 0:
         raise RuntimeError(err.value.decode())
     return out

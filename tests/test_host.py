@@ -198,7 +198,7 @@ def test_python_decode_refuses_host_tensors():
 
 
 def call_prefill(lib, case, *, q=None, out=None, key_cache=None, value_cache=None, bt=None, seq_lens=None,
-                 q_abs=None):
+                 q_abs=None, entry="pth_fa_forward"):
     q = kvc.prefill_query(case) if q is None else q
     B, hq, sq = q.shape[0], q.shape[1], q.shape[2]
     out = torch.empty((B, sq, hq, 256), dtype=torch.float32) if out is None else out
@@ -209,13 +209,18 @@ def call_prefill(lib, case, *, q=None, out=None, key_cache=None, value_cache=Non
     descs = [pth_dec.describe(t) for t in tensors]
     qa, od = pth_dec.describe(q_abs), pth_dec.describe(out)
     err = ctypes.create_string_buffer(256)
-    rc = lib.pth_fa_forward(*[ctypes.byref(x) for x in descs], case.scale, ctypes.byref(qa), ctypes.byref(od), None,
-                            err, len(err))
+    rc = getattr(lib, entry)(*[ctypes.byref(x) for x in descs], case.scale, ctypes.byref(qa), ctypes.byref(od), None,
+                             err, len(err))
     return rc, err.value.decode()
 
 
-def test_prefill_validation_messages(lib):
-    """Messages of forward_pth's checks (kernels/fa_pth/pth_fa.cpp:44-68) and of this boundary's own."""
+PREFILL_ENTRIES = ["pth_fa_forward", "pth_fa_forward_exact"]
+
+
+@pytest.mark.parametrize("entry", PREFILL_ENTRIES)
+def test_prefill_validation_messages(lib, entry):
+    """Messages of forward_pth's checks (kernels/fa_pth/pth_fa.cpp:44-68) and of this boundary's own;
+    pth_fa_forward_exact runs the same checks."""
     case = make(ctxs=[40, 9], qlens=[3, 3])
     q = kvc.prefill_query(case)
     B, hq, sq = q.shape[0], q.shape[1], q.shape[2]
@@ -237,14 +242,15 @@ def test_prefill_validation_messages(lib):
         (dict(out=torch.empty((B * sq * hq * 256 + 1,))[1:].view(B, sq, hq, 256)), "16-byte aligned"),
     ]
     for kw, msg in cases:
-        rc, text = call_prefill(lib, case, **kw)
+        rc, text = call_prefill(lib, case, entry=entry, **kw)
         assert rc == 1 and msg in text, (list(kw.keys()), rc, text)
 
 
-def test_prefill_empty_chunk_is_noop(lib):
+@pytest.mark.parametrize("entry", PREFILL_ENTRIES)
+def test_prefill_empty_chunk_is_noop(lib, entry):
     case = make(ctxs=[40, 9], qlens=[3, 3])
     q = kvc.prefill_query(case)[:, :, :0].contiguous()
-    rc, text = call_prefill(lib, case, q=q, out=torch.empty((2, 0, 12, 256)))
+    rc, text = call_prefill(lib, case, q=q, out=torch.empty((2, 0, 12, 256)), entry=entry)
     assert rc == 0, text
 
 

@@ -36,11 +36,11 @@ def oracle_of(c, q_abs, rows=None):
                              c.cache.v_scale, c.block_table, c.seq_lens, c.scale, torch.tensor(q_abs), rows)
 
 
-def gpu_prefill(d, q_abs):
+def gpu_prefill(d, q_abs, exact=False):
     q = kvc.prefill_query(d)
     out = torch.full((q.shape[0], q.shape[2], q.shape[1], 256), float("nan"), dtype=torch.float32, device="cuda")
     pth_dec.forward_pth(q, d.cache.key_cache, d.cache.value_cache, d.block_table, d.seq_lens, d.scale,
-                        torch.tensor(q_abs, dtype=torch.int32, device="cuda"), out=out)
+                        torch.tensor(q_abs, dtype=torch.int32, device="cuda"), out=out, exact=exact)
     torch.cuda.synchronize()
     return out
 
@@ -100,14 +100,15 @@ def torch_prefill_fp32(d, q_abs):
     return out
 
 
-def test_chunk_of_2048_over_61440_cached():
-    """Config 5 at full size: 32 rows against the float64 oracle, and every one of the 2,048 x 24
-    rows against the fp32 torch reference, which must itself agree with the oracle on those 32
-    rows to 1e-5."""
+@pytest.mark.parametrize("exact", [False, True], ids=["default", "exact"])
+def test_chunk_of_2048_over_61440_cached(exact):
+    """A 2,048-token chunk over 61,440 cached keys at full size: 32 rows against the float64
+    oracle, and every one of the 2,048 x 24 rows against the fp32 torch reference, which must
+    itself agree with the oracle on those 32 rows to 1e-5."""
     c = kvc.make_case([61440], [2048], num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=1005)
-    say("prefill 2048 over 61440, bs 16")
+    say(f"prefill 2048 over 61440, bs 16, exact={exact}")
     d = c.to("cuda")
-    out = gpu_prefill(d, [61440])
+    out = gpu_prefill(d, [61440], exact)
     rng = np.random.default_rng(5)
     rows = sorted(set([0, 1, 31, 32, 2047] + rng.choice(2048, 27, replace=False).tolist()))
     ref, written = oracle_of(c, [61440], rows)
@@ -190,6 +191,62 @@ def test_outlier_rows_within_fp16_weight_rounding():
     bound = 2e-3 + 2.0 ** -11 * mag[written]
     say(f"  max-abs {err.max():.2e} max |ref| {np.abs(ref[written]).max():.1f} worst err/bound {(err / bound).max():.3f}")
     assert (err <= bound).all()
+
+
+def test_exact_outlier_rows_within_decode_tolerance():
+    """pth_fa_forward_exact on the outlier case above: K is widened without bias and P' is
+    carried as fp16 hi + lo, so the P' rounding (2^-12 relative per weight, times |V| up to 50
+    v_scale) drops to ~2^-23 and the plain bar holds: max-abs <= 2e-3, mean-abs <= 2e-4. A second
+    case puts 2% of the rows at 100x, with a 640-key context and the chunk inside the cache."""
+    for ctxs, q_abs, frac, mult, seed in [([3000, 517], [3000, 400], 0.01, 50.0, 41),
+                                          ([640, 2900], [600, 2900], 0.02, 100.0, 43)]:
+        c = kvc.make_case(ctxs, [70] * 2, num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=seed,
+                          outlier_frac=frac, outlier_mult=mult)
+        say(f"exact prefill outliers {frac} x{mult}")
+        d = c.to("cuda")
+        out = gpu_prefill(d, q_abs, exact=True)
+        ref, written = oracle_of(c, q_abs)
+        emax, emean = errors(out, ref, written)
+        dmax, dmean = errors(gpu_prefill(d, q_abs), ref, written)
+        say(f"  exact: max-abs {emax:.2e} mean-abs {emean:.2e}; default: max-abs {dmax:.2e} mean-abs {dmean:.2e}; "
+            f"max |ref| {np.abs(ref[written]).max():.1f}")
+        assert torch.isfinite(out).all()
+        assert emax <= 2e-3 and emean <= 2e-4, (ctxs, emax, emean)
+
+
+EXACT_CASES = [REF_CASES[i] for i in (0, 2, 3, 4, 6)]
+
+
+@pytest.mark.parametrize("ctx,n,nhd", EXACT_CASES, ids=[f"ref{i}" for i in (0, 2, 3, 4, 6)])
+def test_exact_reference_cases(ctx, n, nhd):
+    c = kvc.make_case([ctx], [n], num_q_heads=HQ, num_kv_heads=HKV, block_size=BS_REF,
+                      layout="NHD" if nhd else "HND", seed=ctx + n, kv_mode="uniform")
+    say(f"exact prefill ctx={ctx} chunk={n} nhd={nhd}")
+    out = gpu_prefill(c.to("cuda"), [ctx], exact=True)
+    rows = None if n <= 800 else list(range(0, 32)) + list(range(n - 32, n)) + list(range(100, n, 97))
+    ref, written = oracle_of(c, [ctx], rows)
+    emax, emean = errors(out, ref, written)
+    say(f"  max-abs {emax:.2e} mean-abs {emean:.2e}")
+    assert torch.isfinite(out).all()
+    assert emax <= 2e-3 and emean <= 2e-4, (ctx, n, emax, emean)
+
+
+@pytest.mark.parametrize("bs,layout,hq,hkv", [(16, "HND", 24, 4), (8, "NHD", 28, 4), (1, "HND", 8, 8),
+                                              (48, "NHD", 48, 2)])
+def test_exact_batches_and_group_sizes(bs, layout, hq, hkv):
+    """The exact entry on the batch shapes of the default's tests: chunk offsets before the first
+    key, inside and past the cache, rows that see no key (written as 0), and G = 6, 7, 1, 24."""
+    ctxs, sq = [3000, 0, 517], 70
+    c = kvc.make_case(ctxs, [sq] * 3, num_q_heads=hq, num_kv_heads=hkv, block_size=bs, layout=layout,
+                      seed=200 + bs + hq)
+    q_abs = [3000, -20, 700]
+    say(f"exact prefill batch bs={bs} layout={layout} hq={hq} hkv={hkv}")
+    out = gpu_prefill(c.to("cuda"), q_abs, exact=True)
+    ref, written = oracle_of(c, q_abs)
+    emax, emean = errors(out, ref, written)
+    say(f"  max-abs {emax:.2e} mean-abs {emean:.2e}")
+    assert emax <= 2e-3 and emean <= 2e-4, (emax, emean)
+    assert (out.cpu().numpy()[~written] == 0).all()
 
 
 @pytest.mark.parametrize("bs", [16, 8])

@@ -162,8 +162,21 @@ def draw_prefill(i):
 
 @pytest.mark.parametrize("i", range(N_PREFILL))
 def test_prefill_random(i):
+    run_prefill_case(i, exact=False)
+
+
+N_PREFILL_EXACT = 12
+
+
+@pytest.mark.parametrize("i", range(N_PREFILL, N_PREFILL + N_PREFILL_EXACT))
+def test_prefill_random_exact(i):
+    """pth_fa_forward_exact on cases drawn like the default's (other seeds), to the same bar."""
+    run_prefill_case(i, exact=True)
+
+
+def run_prefill_case(i, exact):
     p = draw_prefill(i)
-    say(f"prefill sweep {i}: {p}")
+    say(f"prefill sweep {i} exact={exact}: {p}")
     c = kvc.make_case(p["ctxs"], [p["sq"]] * len(p["ctxs"]), num_q_heads=p["hq"], num_kv_heads=p["hkv"],
                       block_size=p["bs"], layout=p["layout"], seed=p["seed"], kv_mode=p["kv_mode"])
     ref, written = orc.paged_prefill(kvc.prefill_query(c), c.cache.key_cache, c.cache.value_cache, c.cache.k_scale,
@@ -175,7 +188,7 @@ def test_prefill_random(i):
     before = fingerprint(*inputs)
     wo, out = guarded((q.shape[0], q.shape[2], q.shape[1], 256), torch.float32, float("nan"))
     pth_dec.forward_pth(q, d.cache.key_cache, d.cache.value_cache, d.block_table, d.seq_lens, d.scale,
-                        torch.tensor(p["q_abs"], dtype=torch.int32, device="cuda"), out=out)
+                        torch.tensor(p["q_abs"], dtype=torch.int32, device="cuda"), out=out, exact=exact)
     torch.cuda.synchronize()
     assert guards_intact(wo), "a write outside the output"
     assert fingerprint(*inputs) == before, "an input was written"
