@@ -10,6 +10,9 @@
 //                registers, K and V operands read from the fp16 buffer.
 // One barrier per tile orders the three stages. There is no split: each row is normalised in
 // registers and stored once. Q arrives as fp32 and is rounded to fp16 for the MFMA.
+// kExact (pth_fa_forward_exact) gives the decode kernel's numerics: K is widened without the
+// bias (so the fp32 score accumulators hold only partial scores) and P' enters the P.V products
+// as fp16 hi + lo, which doubles them.
 #include <type_traits>
 
 #include "pd_tile.hpp"
