@@ -21,7 +21,9 @@ few fields the routing reads.
 - forward_pth_fa (triton_attn.patch:176-262): the sequences with >= MIN_Q query tokens must form
   a suffix of the batch; the rows before it go to the decode operator when every prefix sequence
   has <= 4 (8 with DFlash) query tokens, else to the caller's Triton function. Each suffix
-  sequence runs the prefill operator once (no padding to a tile ladder is needed).
+  sequence runs the prefill operator once (no padding to a tile ladder is needed);
+  VLLM_GFX950_PTH_FA_EXACT=1 selects its exact entry (pth_fa_forward_exact: the decode's
+  numerics, for caches with very large per-token scales, at ~26 % more time).
 - route (triton_attn.patch:272-308): prefill first when max_seqlen_q >= MIN_Q, then decode
   when max_seqlen_q <= MAX_Q; causal only, no multimodal prefix, no RSWA prefix, no output
   scale. Returns False when the caller must run its own path.
@@ -45,6 +47,7 @@ PTH_FA_MIN_Q = int(os.environ.get("VLLM_GFX950_PTH_FA_MIN_Q", "64"))
 PTH_DEC_MAX_Q = int(os.environ.get("VLLM_GFX950_PTH_DEC_MAX_Q", "4"))
 PTH_DEC_SPLITS = int(os.environ.get("VLLM_GFX950_PTH_DEC_SPLITS", "64"))
 PTH_DEC_CUS = int(os.environ.get("VLLM_GFX950_PTH_DEC_CUS", "0"))  # 0: the device's CU count
+PTH_FA_EXACT = os.environ.get("VLLM_GFX950_PTH_FA_EXACT", "0") == "1"  # prefill through pth_fa_forward_exact
 MAX_ROWS_PER_KV_HEAD = 48  # qmax * G the decode operator takes
 
 _dec_mod = None
@@ -269,7 +272,7 @@ class Gfx950Int8Attention:
             q = query[start:start + nq].transpose(0, 1).unsqueeze(0).float().contiguous()  # [1, Hq, nq, D]
             seq_len = meta.seq_lens[i:i + 1]
             out = self.pth_fa.forward_pth(q, key_cache, value_cache, meta.block_table[i:i + 1], seq_len, self.scale,
-                                          seq_len - nq)
+                                          seq_len - nq, **({"exact": True} if PTH_FA_EXACT else {}))
             output[start:start + nq] = out[0].to(output.dtype)
         return True
 

@@ -26,8 +26,9 @@ class FakeOps:
         self.calls.append(("decode", q.shape[0], num_seqs, qmax, nsplit, window, bt.shape[0]))
         out.fill_(1.0)
 
-    def forward_pth(self, q, kc, vc, bt, sl, scale, q_abs):
+    def forward_pth(self, q, kc, vc, bt, sl, scale, q_abs, exact=False):
         self.calls.append(("prefill", tuple(q.shape), int(sl[0]), int(q_abs[0]), q.dtype))
+        self.exact = getattr(self, "exact", []) + [exact]
         return torch.full((1, q.shape[2], q.shape[1], q.shape[3]), 2.0)
 
 
@@ -203,6 +204,18 @@ def test_prefill_suffix_with_decode_prefix(ops):
     assert pre == [("prefill", (1, 24, 100, 256), 1100, 1000, torch.float32),
                    ("prefill", (1, 24, 70, 256), 70, 0, torch.float32)]
     assert (out[:2] == 1).all() and (out[2:] == 2).all()
+
+
+@pytest.mark.parametrize("exact", [False, True])
+def test_prefill_exact_switch(ops, monkeypatch, exact):
+    """VLLM_GFX950_PTH_FA_EXACT=1 (read at import into PTH_FA_EXACT) sends every prefill call to
+    the exact entry; by default the call carries no exact flag."""
+    monkeypatch.setattr(shim, "PTH_FA_EXACT", exact)
+    a = impl()
+    q, out, kc = tensors(100 + 70)
+    m = meta([100, 70], [1100, 70])
+    assert a.route(q, kc, kc, None, None, m, out, 100, 170, lambda *x: pytest.fail("fallback"))
+    assert ops.exact == [exact, exact]
 
 
 def test_prefill_prefix_too_long_for_decode_goes_to_triton(ops):
