@@ -22,6 +22,8 @@ summaries committed under profiles/ for the same workload.
   4  long context, 1 x 4 tokens, ctx 200,000, 1 % of the (token, kv head) rows x 50 before
      quantisation: one call captured in a HIP graph and the graph replayed 1,000 times
   5  chunked prefill, a 2,048-token causal chunk over 61,440 cached tokens (63,488 keys)
+  w  the KV-cache writer (pth_cache_write) on 4, 2,048 and 32,768 new tokens (fp16 K/V as
+     strided views of a fused QKV buffer): µs per call, algorithmic GB/s, fraction of 8 TB/s
 Decode configs report µs per layer, algorithmic GB/s and the fraction of 8 TB/s; the prefill
 reports ms per chunk and TFLOP/s against the 2.5 PFLOP/s dense fp16 MFMA peak. The split count
 of each decode config is the one the vLLM shim picks (vllm_shim.decode_splits with the host-side
@@ -86,11 +88,11 @@ def summarize_traffic(args):
     for counter, run_dir in (("FETCH_SIZE", args.traffic_summary[0]), ("WRITE_SIZE", args.traffic_summary[1])):
         d = _pmc_dispatches(run_dir, counter)
         order = sorted(d)
-        part = [d[k][1] for k in order if "partial" in d[k][0]]
+        part = [d[k][1] for k in order if args.traffic_kernel in d[k][0]]
         other = [d[k][1] for k in order if not d[k][0].startswith("pd_")]
         calib = other[-CALIB_COPIES:]
         if not part or len(calib) < CALIB_COPIES:
-            raise SystemExit(f"{counter}: {len(part)} partial dispatches, {len(calib)} calibration copies")
+            raise SystemExit(f"{counter}: {len(part)} {args.traffic_kernel} dispatches, {len(calib)} calibration copies")
         part.sort()
         calib.sort()
         p_kib, c_kib = part[len(part) // 2], calib[len(calib) // 2]
@@ -98,8 +100,12 @@ def summarize_traffic(args):
         res[counter] = {"partial_kib_median": p_kib, "calib_copy_kib_median": c_kib, "calib_factor": factor,
                         "partial_bytes": p_kib * 1024.0 * factor, "dispatches": len(part)}
     total = res["FETCH_SIZE"]["partial_bytes"] + res["WRITE_SIZE"]["partial_bytes"]
-    summary = {"kernel": "decode partial kernel", "workload": "MTP verify 4 x 24/4 heads, ctx 61440+4, bs 16",
-               "nsplit": args.nsplit, "hbm_bytes_per_launch": round(total), "counters": res,
+    if args.traffic_kernel == "partial":
+        what = {"kernel": "decode partial kernel", "workload": "MTP verify 4 x 24/4 heads, ctx 61440+4, bs 16",
+                "nsplit": args.nsplit}
+    else:
+        what = {"kernel": args.traffic_kernel, "workload": args.traffic_workload}
+    summary = {**what, "hbm_bytes_per_launch": round(total), "counters": res,
                "calibration": f"{CALIB_COPIES} copies of {CALIB_BYTES} bytes (read + write) after the partial "
                               f"launches; factor = known bytes / counter bytes"}
     with open(args.traffic_out, "w") as f:
@@ -140,6 +146,17 @@ def summarize_counters(args):
     with open(args.counters_out, "w") as f:
         json.dump(summary, f, indent=1)
     print(json.dumps(summary))
+
+
+def calibration_copies(torch, dev):
+    """CALIB_COPIES plain copies of CALIB_BYTES (read and written once each): the known sizes the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE readings are scaled by."""
+    src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(CALIB_COPIES):
+        dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 def load_package():
@@ -343,7 +360,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=200, help="untimed operator calls before them")
     ap.add_argument("--nsplit", type=int, default=64, help="config 2 split count")
     ap.add_argument("--rotate", type=int, default=8, help="distinct config-2 KV caches cycled through")
-    ap.add_argument("--configs", default="1,3,4,5", help="other configs to measure ('' for none)")
+    ap.add_argument("--configs", default="1,3,4,5,w",
+                    help="other configs to measure, 'w' for the KV-cache writer ('' for none)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=5)
     ap.add_argument("--profile-only", action="store_true",
@@ -353,8 +371,14 @@ def main():
                     help="no GPU work: turn two rocprofv3 --pmc runs of --profile-only (FETCH_SIZE, WRITE_SIZE) "
                          "into HBM bytes per partial launch, written to --traffic-out")
     ap.add_argument("--traffic-out", default=os.path.join(PROFILES, "pd_partial_mtp61k_traffic.json"))
+    ap.add_argument("--traffic-kernel", default="partial",
+                    help="substring of the kernel name whose dispatches --traffic-summary reads")
+    ap.add_argument("--traffic-workload", default="", help="workload description for --traffic-summary")
     ap.add_argument("--profile-prefill", type=int, default=0, metavar="N",
                     help="run N config-5 prefill chunks (alternating two cache copies) and nothing else, for "
+                         "rocprofv3")
+    ap.add_argument("--profile-kvwrite", type=int, default=0, metavar="N",
+                    help="run N KV-cache writer calls on the largest writer workload and nothing else, for "
                          "rocprofv3")
     ap.add_argument("--counters-summary", metavar="PMC_DIR",
                     help="no GPU work: turn a rocprofv3 --pmc run of --profile-only with the counters in "
@@ -397,6 +421,13 @@ def main():
         bench_grid(torch, wl, pd, pkg.vllm_shim, dev, stream, hq, hkv, bs)
         return
 
+    if args.profile_kvwrite:
+        res = bench_cache_write(torch, wl, pd, dev, stream, KVW_TOKENS[-1], reps=1, calls=args.profile_kvwrite)
+        calibration_copies(torch, dev)
+        print(json.dumps({"profile_kvwrite": True, "tokens": KVW_TOKENS[-1], "us_per_call": res["us_per_call"],
+                          "GB_s": res["GB_s"], "calib_copies": CALIB_COPIES, "calib_bytes": CALIB_BYTES}))
+        return
+
     if args.profile_prefill:
         res = bench_prefill(torch, wl, pd, dev, stream, reps=2 * max(1, args.profile_prefill // 2))
         print(json.dumps({"profile_prefill": True, "chunks": 2 * max(1, args.profile_prefill // 2) + 4,
@@ -417,12 +448,7 @@ def main():
         with torch.cuda.stream(stream):
             g.replay()
         torch.cuda.synchronize()
-        src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        for _ in range(CALIB_COPIES):
-            dst.copy_(src)
-        torch.cuda.synchronize()
+        calibration_copies(torch, dev)
         print(json.dumps({"profile_only": True, "partial_launches": args.steps, "nsplit": args.nsplit,
                           "calib_copies": CALIB_COPIES, "calib_bytes": CALIB_BYTES}))
         return
@@ -447,7 +473,8 @@ def main():
     traffic = traffic_j.get("hbm_bytes_per_launch") if traffic_j and traffic_j.get("nsplit") == args.nsplit else None
     counters = committed_profile("pd_partial_mtp61k_counters.json")
 
-    want = [int(x) for x in args.configs.split(",") if x.strip()]
+    want = [int(x) for x in args.configs.split(",") if x.strip().isdigit()]
+    want_kvw = "w" in [x.strip() for x in args.configs.split(",")]
     configs = {}
     shim = pkg.vllm_shim
     for n in (1, 3, 4):
@@ -480,6 +507,8 @@ def main():
         torch.cuda.empty_cache()
     if 5 in want:
         configs["5"] = bench_prefill(torch, wl, pd, dev, stream)
+    if want_kvw:
+        configs["kv_write"] = {str(T): bench_cache_write(torch, wl, pd, dev, stream, T) for T in KVW_TOKENS}
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -561,6 +590,58 @@ def bench_prefill(torch, wl, pd, dev, stream, reps=20):
     return {"workload": DESCRIPTIONS[5], "ms_per_chunk": round(ms, 4), "TFLOP_s": round(tflops, 1),
             "frac": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4), "flops": flops, "peak": MFMA_FP16_PEAK_TFLOPS,
             "bound": "mfma", "timed": f"{reps // 2} replays of a 2-call graph over 2 cache copies"}
+
+
+KVW_TOKENS = (4, 2048, 32768)
+
+
+def bench_cache_write(torch, wl, pd, dev, stream, T, reps=None, calls=None):
+    """The KV-cache writer (pth_cache_write) on T new tokens of one sequence: key and value fp16
+    [T, 4, 256] as the strided views vLLM hands over (slices of one fused QKV projection output
+    [T, (24 + 2 x 4) x 256]), slots at positions 0..T-1 of a sequence whose 16-slot blocks are a
+    random permutation of the cache's, HND layout. Inputs and caches rotate over enough copies that
+    every call reads and writes HBM rather than the 256 MB Infinity Cache. Bytes: K and V read
+    (2 x T x 4 x 512), the slot mapping (8 T), the rows written (T x 4 x 520)."""
+    hq, hkv, D, bs = 24, 4, 256, 16
+    read = 2 * T * hkv * D * 2 + 8 * T
+    write = T * hkv * 520
+    copies = max(2, min(64, -(-(512 << 20) // (read + write))))
+    g = torch.Generator().manual_seed(77 + T)
+    gd = torch.Generator(device=dev).manual_seed(77 + T)
+    nblk = -(-T // bs)
+    perm = torch.randperm(nblk, generator=g)
+    pos = torch.arange(T)
+    slots = (perm[pos // bs] * bs + pos % bs).to(torch.int64).to(dev)
+    qkvs, caches = [], []
+    for i in range(copies):
+        qkvs.append(torch.randn((T, (hq + 2 * hkv) * D), generator=gd, device=dev, dtype=torch.float16))
+        caches.append(wl.allocate_cache(nblk, bs, hkv, "HND", device=dev))
+
+    def op(i):
+        qkv, c = qkvs[i], caches[i]
+        k = qkv[:, hq * D:(hq + hkv) * D].view(T, hkv, D)
+        v = qkv[:, (hq + hkv) * D:].view(T, hkv, D)
+        return lambda: pd.cache_write(k, v, c.key_cache, c.value_cache, c.k_scale, c.v_scale, slots)
+
+    with torch.cuda.stream(stream):
+        for i in range(copies):
+            op(i)()
+    torch.cuda.synchronize()
+    per = calls or copies
+    gr = graph_of(torch, stream, [op(i % copies) for i in range(per)])
+    reps = reps or max(3, 4000 // per)
+    with torch.cuda.stream(stream):
+        gr.replay()
+        ms = time_replays(torch, gr, reps, stream)
+    us = ms * 1e3 / (reps * per)
+    gbs = (read + write) / (us * 1e-6) / 1e9
+    del gr, qkvs, caches
+    torch.cuda.empty_cache()
+    return {"tokens": T, "us_per_call": round(us, 3), "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": read + write,
+            "workload": f"KV-cache writer: {T} tokens x 4 kv heads, fp16 K/V as strided views of a fused QKV "
+                        f"buffer, random 16-slot pages, HND",
+            "timed": f"{reps} replays of a {per}-call graph over {copies} input/cache copies"}
 
 
 def cpu_prefill_baseline(torch, wl, orc, nrows=24):

@@ -179,8 +179,8 @@ int pth_fa_forward_exact(const pd_tensor* q, const pd_tensor* key_cache, const p
  *   slot_mapping int64 [T]: slot = block * block_size + offset; negative slots (padding) and
  *                slots past the cache are skipped
  * Per (token, kv head): scale = absmax / 127 (0 for an all-zero row), q = clamp(rint(x / scale),
- * -127, 127) with x / scale correctly rounded. Returns 0, 1 (validation failure, message in
- * err) or 2 (launch failure).
+ * -127, 127) with x / scale correctly rounded. At most 2^30 (token, kv head) rows per call.
+ * Returns 0, 1 (validation failure, message in err) or 2 (launch failure).
  */
 int pth_cache_write(const pd_tensor* key, const pd_tensor* value, const pd_tensor* key_cache,
                     const pd_tensor* value_cache, const pd_tensor* k_scale, const pd_tensor* v_scale,

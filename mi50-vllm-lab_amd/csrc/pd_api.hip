@@ -360,6 +360,7 @@ int pth_cache_write(const pd_tensor* key, const pd_tensor* value, const pd_tenso
           key->sizes[2] == 256 && value->sizes[2] == 256 && value->sizes[0] == T && key->strides[2] == 1 &&
           value->strides[2] == 1))
         return fail(err, errlen, "key and value must be [T, Hkv, 256] with unit dim stride");
+    if (T * Hkv > ((int64_t)1 << 30)) return fail(err, errlen, "at most 2^30 (token, kv head) rows per call");
     const int64_t esz = dt == PD_DTYPE_FP32 ? 4 : 2;
     const int64_t vec = 4 * esz;  // each lane loads 4 elements
     if (!((reinterpret_cast<uintptr_t>(key->data) % vec) == 0 && (reinterpret_cast<uintptr_t>(value->data) % vec) == 0 &&

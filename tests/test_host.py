@@ -282,6 +282,8 @@ def test_cache_write_validation_messages(lib):
         (dict(key=torch.zeros((3, 2, 512), dtype=torch.float16)[..., ::2]), "[T, Hkv, 256]"),
         (dict(slot_mapping=slots.int()), "int64 [T]"),
         (dict(slot_mapping=slots[:2]), "int64 [T]"),
+        # more than 2^30 (token, kv head) rows (a stride-0 view: nothing is allocated or read)
+        (dict(key=torch.zeros((1, 2, 256), dtype=torch.float16).expand(1 << 29 | 1, 2, 256), value=torch.zeros((1, 2, 256), dtype=torch.float16).expand(1 << 29 | 1, 2, 256)), "at most 2^30"),
     ]
     for kw, msg in cases:
         rc, text = call(**kw)
