@@ -204,6 +204,9 @@ int pth_dec_decode(const pd_tensor* q, const pd_tensor* key_cache, const pd_tens
     if (!(out->dtype == PD_DTYPE_FP16 && out->ndim == 3 && out->sizes[0] == q->sizes[0] &&
           out->sizes[1] == q->sizes[1] && out->sizes[2] == 256 && out->strides[2] == 1))
         return fail(err, errlen, "out must be fp16 [T, Hq, 256] with unit dim stride");
+    if (!(q->sizes[0] <= INT32_MAX && q->sizes[1] <= INT32_MAX && num_seqs <= INT32_MAX && qmax <= INT32_MAX &&
+          nsplit <= INT32_MAX && window >= INT32_MIN && window <= INT32_MAX))
+        return fail(err, errlen, "sizes, num_seqs, qmax, nsplit and window must fit in 32 bits");
     if (!layout_ok(key_cache, value_cache, k_scale, v_scale))
         return fail(err, errlen, "KV cache views do not have the int8 per-token-head row layout");
     if (!(block_table->dtype == PD_DTYPE_INT32 && seq_lens->dtype == PD_DTYPE_INT32 &&
@@ -217,7 +220,8 @@ int pth_dec_decode(const pd_tensor* q, const pd_tensor* key_cache, const pd_tens
     const int64_t T = q->sizes[0], Hq = q->sizes[1], Hkv = key_cache->sizes[2];
     const int64_t nseg = part_o->sizes[2];
     if (!(part_o->sizes[0] >= T && part_o->sizes[1] == Hq && part_m->sizes[0] >= T && part_m->sizes[1] == Hq &&
-          part_m->sizes[2] == nseg && part_l->sizes[0] >= T && part_l->sizes[1] == Hq && part_l->sizes[2] == nseg))
+          part_m->sizes[2] == nseg && part_l->sizes[0] >= T && part_l->sizes[1] == Hq && part_l->sizes[2] == nseg &&
+          nseg <= INT32_MAX))
         return fail(err, errlen, "partial buffers too small");
     if (!(Hkv > 0 && Hq % Hkv == 0)) return fail(err, errlen, "heads_q must be a multiple of heads_kv");
     if (!(qmax >= 1 && qmax * (Hq / Hkv) <= 16 * kMaxRowBlocks))
@@ -263,6 +267,8 @@ static int fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_t
         return fail(err, errlen, "block_table/seq_lens/q_abs_offset must be int32");
     const int64_t B = q->sizes[0], Hq = q->sizes[1], Sq = q->sizes[2], D = q->sizes[3];
     const int64_t bs = key_cache->sizes[1], Hkv = key_cache->sizes[2];
+    if (!(B <= INT32_MAX && Hq <= INT32_MAX && Sq <= INT32_MAX))
+        return fail(err, errlen, "B, Hq and Sq must be below 2^31");
     if (D != 256) return fail(err, errlen, "head_dim must be 256 (only instantiation built)");
     if (!(key_cache->sizes[3] >= D + 4 && value_cache->sizes[3] >= D + 4))
         return fail(err, errlen, "cache rows must hold D int8 values and a fp32 scale");

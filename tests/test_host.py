@@ -100,7 +100,7 @@ def test_supported_layout_rejects():
 
 
 def call_decode(lib, case, *, q=None, out=None, bt=None, part=None, num_seqs=None, qmax=None, nsplit=4,
-                key_cache=None):
+                key_cache=None, window=-1):
     q = case.q if q is None else q
     T, hq = q.shape[0], q.shape[1]
     out = torch.empty((T, hq, 256), dtype=torch.float16) if out is None else out
@@ -113,7 +113,7 @@ def call_decode(lib, case, *, q=None, out=None, bt=None, part=None, num_seqs=Non
     err = ctypes.create_string_buffer(256)
     rc = lib.pth_dec_decode(*[ctypes.byref(x) for x in descs], case.scale, *[ctypes.byref(x) for x in pdescs],
                             case.num_seqs if num_seqs is None else num_seqs, case.qmax if qmax is None else qmax,
-                            nsplit, -1, 1, None, err, len(err))
+                            nsplit, window, 1, None, err, len(err))
     return rc, err.value.decode()
 
 
@@ -135,6 +135,11 @@ def test_decode_validation_messages(lib):
         (dict(nsplit=9), "nsplit must be in [1, NSEG]"),
         (dict(nsplit=0), "nsplit must be in [1, NSEG]"),
         (dict(num_seqs=3), "per-sequence tensors too small"),
+        # sizes and scalars that would be truncated to 32 bits (stride-0 views: nothing allocated)
+        (dict(q=case.q[:1].expand(1 << 31, hq, 256), out=torch.empty((1, hq, 256), dtype=torch.float16).expand(
+            1 << 31, hq, 256), part=kvc.partial_buffers(T, hq, 8, "cpu")), "must fit in 32 bits"),
+        (dict(window=1 << 31), "must fit in 32 bits"),
+        (dict(num_seqs=1 << 32), "must fit in 32 bits"),
     ]
     for kw, msg in cases:
         rc, text = call_decode(lib, case, **kw)
@@ -244,6 +249,32 @@ def test_prefill_validation_messages(lib, entry):
     for kw, msg in cases:
         rc, text = call_prefill(lib, case, entry=entry, **kw)
         assert rc == 1 and msg in text, (list(kw.keys()), rc, text)
+
+
+@pytest.mark.parametrize("entry", PREFILL_ENTRIES)
+def test_prefill_rejects_sizes_beyond_32_bits(lib, entry):
+    """A chunk of 2^31 query tokens is refused before anything is read: the descriptors claim
+    that size over small real buffers, which the checks never dereference."""
+    case = make(ctxs=[40, 9], qlens=[3, 3])
+    q = kvc.prefill_query(case)
+    B, hq = q.shape[0], q.shape[1]
+    big = 1 << 31
+    qd = pth_dec.describe(q)
+    qd.sizes[2] = big
+    for i, st in enumerate((hq * big * 256, big * 256, 256, 1)):
+        qd.strides[i] = st
+    out = torch.empty((B, 3, hq, 256))
+    od = pth_dec.describe(out)
+    od.sizes[1] = big
+    for i, st in enumerate((big * hq * 256, hq * 256, 256, 1)):
+        od.strides[i] = st
+    c = case.cache
+    descs = [pth_dec.describe(t) for t in (c.key_cache, c.value_cache, case.block_table, case.seq_lens)]
+    qa = pth_dec.describe(torch.tensor(case.ctxs, dtype=torch.int32))
+    err = ctypes.create_string_buffer(256)
+    rc = getattr(lib, entry)(ctypes.byref(qd), *[ctypes.byref(x) for x in descs], case.scale, ctypes.byref(qa),
+                             ctypes.byref(od), None, err, len(err))
+    assert rc == 1 and "below 2^31" in err.value.decode(), (rc, err.value)
 
 
 @pytest.mark.parametrize("entry", PREFILL_ENTRIES)
