@@ -142,8 +142,11 @@ hipError_t pth_dec_launch_noalloc(const void* q, int q_st, const void* kc, int k
     hipError_t e = check_args(x, false);
     if (e != hipSuccess) return e;
     if (num_tokens == 0) return hipSuccess;
-    const size_t rows = (size_t)num_tokens * (size_t)heads_q * (size_t)nsplit;
-    if (rows * (kDim + 2) * sizeof(float) > kScratchBytes) return hipErrorOutOfMemory;
+    // partial rows the array holds; the product is bounded in two steps so that it cannot wrap
+    const uint64_t max_rows = kScratchBytes / ((kDim + 2) * sizeof(float));
+    const uint64_t th = (uint64_t)num_tokens * (uint64_t)heads_q;  // both below 2^31
+    if (th > max_rows || th * (uint64_t)nsplit > max_rows) return hipErrorOutOfMemory;
+    const size_t rows = (size_t)(th * (uint64_t)nsplit);
     void* base = nullptr;
     e = scratch_address(&base);
     if (e != hipSuccess) return e;

@@ -152,6 +152,16 @@ def test_decode_validation_messages(lib):
     del q5
 
 
+def test_noalloc_size_check_cannot_wrap(lib):
+    """num_tokens x heads_q x nsplit = 2^16 x (48 x 2^20) x 2^24 = 3 x 2^64: a 64-bit product wraps
+    to 0 and would pass the 32 MiB limit. The entry point must refuse it (hipErrorOutOfMemory, 2)
+    before it touches a device; the arguments pass every other check (G = 48, qmax 1)."""
+    heads_kv, heads_q, nsplit, num_tokens = 1 << 20, 48 << 20, 1 << 24, 1 << 16
+    rc = lib.pth_dec_launch_noalloc(None, 256, None, 8320, 520, 33280, None, 1, None, None, 1, num_tokens, heads_q,
+                                    heads_kv, 16, 0.0625, 1, nsplit, None, 0, 0, None, -1, 1)
+    assert rc == 2, rc
+
+
 def test_decode_empty_batch_is_noop(lib):
     case = make()
     q0 = case.q[:0]
