@@ -124,7 +124,8 @@ int pth_dec_supported_layout(const pd_tensor* key_cache, const pd_tensor* value_
 
 /*
  * The torch op `decode` of kernels/pth_dec/pth_dec.cpp:49-91 over descriptors, with window
- * and causal appended. Validates every tensor like the reference's TORCH_CHECKs; on failure
+ * and causal appended. Validates every tensor like the reference's TORCH_CHECKs (and refuses
+ * sizes, counts or a window that do not fit in 32 bits); on failure
  * returns 1 and writes the reference's message into err (errlen bytes, NUL-terminated);
  * returns 2 with the HIP error string if the launch fails; 0 on success.
  */
@@ -147,8 +148,8 @@ const char* pth_dec_version(void);
  *   key_cache / value_cache  the cache views (value_cache = key_cache + 260 bytes)
  *   block_table  int32 [B, max_blocks]; seq_lens, q_abs_offset int32 [B]
  *   out          fp32 [B, Sq, Hq, 256], unit dim stride
- * Q is rounded to fp16 for the matrix cores; scores and P.V accumulate in fp32. Returns 0, 1
- * (validation failure, message in err) or 2 (launch failure).
+ * Q is rounded to fp16 for the matrix cores; scores and P.V accumulate in fp32. B, Hq and Sq
+ * must be below 2^31. Returns 0, 1 (validation failure, message in err) or 2 (launch failure).
  */
 int pth_fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_tensor* value_cache,
                    const pd_tensor* block_table, const pd_tensor* seq_lens, double scale,
