@@ -21,7 +21,8 @@ summaries committed under profiles/ for the same workload.
      2,048-key sliding window, pages outside every window freed (NaN)
   4  long context, 1 x 4 tokens, ctx 200,000, 1 % of the (token, kv head) rows x 50 before
      quantisation: one call captured in a HIP graph and the graph replayed 1,000 times
-  5  chunked prefill, a 2,048-token causal chunk over 61,440 cached tokens (63,488 keys)
+  5  chunked prefill, a 2,048-token causal chunk over 61,440 cached tokens (63,488 keys), through
+     pth_fa_forward and (under `exact`) pth_fa_forward_exact
   w  the KV-cache writer (pth_cache_write) on 4, 2,048 and 32,768 new tokens (fp16 K/V as
      strided views of a fused QKV buffer): µs per call, algorithmic GB/s, fraction of 8 TB/s
 Decode configs report µs per layer, algorithmic GB/s and the fraction of 8 TB/s; the prefill
@@ -429,7 +430,7 @@ def main():
         return
 
     if args.profile_prefill:
-        res = bench_prefill(torch, wl, pd, dev, stream, reps=2 * max(1, args.profile_prefill // 2))
+        res = bench_prefill(torch, wl, pd, dev, stream, reps=2 * max(1, args.profile_prefill // 2), exact_too=False)
         print(json.dumps({"profile_prefill": True, "chunks": 2 * max(1, args.profile_prefill // 2) + 4,
                           "ms_per_chunk": res["ms_per_chunk"]}))
         return
@@ -564,8 +565,9 @@ def main():
 PREFILL_CTX, PREFILL_CHUNK = 61440, 2048
 
 
-def bench_prefill(torch, wl, pd, dev, stream, reps=20):
-    """Config 5: ms per chunk and TFLOP/s of the chunked-prefill operator."""
+def bench_prefill(torch, wl, pd, dev, stream, reps=20, exact_too=True):
+    """Config 5: ms per chunk and TFLOP/s of the chunked-prefill operator (pth_fa_forward), and
+    of pth_fa_forward_exact on the same chunk under `exact`."""
     ctx, sq = PREFILL_CTX, PREFILL_CHUNK
     case = wl.make_case([ctx], [sq], num_q_heads=24, num_kv_heads=4, block_size=16, seed=1005)
     flops = wl.prefill_flops([ctx + sq], [ctx], sq, 24)
@@ -575,21 +577,31 @@ def bench_prefill(torch, wl, pd, dev, stream, reps=20):
     qa = torch.tensor([ctx], dtype=torch.int32, device=dev)
     out = torch.empty((1, sq, 24, 256), dtype=torch.float32, device=dev)
 
-    def op(c):
-        return lambda: pd.forward_pth(q, c.key_cache, c.value_cache, d.block_table, d.seq_lens, d.scale, qa, out=out)
+    def op(c, exact=False):
+        return lambda: pd.forward_pth(q, c.key_cache, c.value_cache, d.block_table, d.seq_lens, d.scale, qa, out=out,
+                                      exact=exact)
 
-    with torch.cuda.stream(stream):
-        for c in caches:
-            op(c)()
-    torch.cuda.synchronize()
-    g = graph_of(torch, stream, [op(c) for c in caches])
-    with torch.cuda.stream(stream):
-        g.replay()
-        ms = time_replays(torch, g, reps // 2, stream) / reps
+    def timed(exact):
+        with torch.cuda.stream(stream):
+            for c in caches:
+                op(c, exact)()
+        torch.cuda.synchronize()
+        g = graph_of(torch, stream, [op(c, exact) for c in caches])
+        with torch.cuda.stream(stream):
+            g.replay()
+            return time_replays(torch, g, reps // 2, stream) / reps
+
+    ms = timed(False)
     tflops = flops / (ms * 1e-3) / 1e12
-    return {"workload": DESCRIPTIONS[5], "ms_per_chunk": round(ms, 4), "TFLOP_s": round(tflops, 1),
+    line = {"workload": DESCRIPTIONS[5], "ms_per_chunk": round(ms, 4), "TFLOP_s": round(tflops, 1),
             "frac": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4), "flops": flops, "peak": MFMA_FP16_PEAK_TFLOPS,
             "bound": "mfma", "timed": f"{reps // 2} replays of a 2-call graph over 2 cache copies"}
+    if exact_too:
+        mse = timed(True)
+        tfe = flops / (mse * 1e-3) / 1e12
+        line["exact"] = {"entry": "pth_fa_forward_exact", "ms_per_chunk": round(mse, 4), "TFLOP_s": round(tfe, 1),
+                         "frac": round(tfe / MFMA_FP16_PEAK_TFLOPS, 4)}
+    return line
 
 
 KVW_TOKENS = (4, 2048, 32768)
