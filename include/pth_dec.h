@@ -170,6 +170,23 @@ int pth_fa_forward_exact(const pd_tensor* q, const pd_tensor* key_cache, const p
                          int errlen);
 
 /*
+ * No counterpart in the reference. pth_fa_forward (exact != 0: pth_fa_forward_exact) with each
+ * query tile's keys split over nsplit workgroups, for chunks too short to fill the GPU (a
+ * workgroup takes 192 query rows of one kv head, so a 64-token chunk of 24 q / 4 kv heads
+ * launches 8 of them per split). Each split stores unnormalised partials in the caller's
+ * workspace, and a second kernel merges them into out.
+ *   workspace  fp32, contiguous, 16-byte aligned, at least B * Sq * Hq * nsplit * 258 floats
+ *              (ignored when nsplit == 1)
+ *   nsplit     1..64
+ * Other arguments, checks, errors and return codes are those of pth_fa_forward. The results
+ * equal pth_fa_forward's within rounding (the partial sums are merged in another order).
+ */
+int pth_fa_forward_split(const pd_tensor* q, const pd_tensor* key_cache, const pd_tensor* value_cache,
+                         const pd_tensor* block_table, const pd_tensor* seq_lens, double scale,
+                         const pd_tensor* q_abs_offset, const pd_tensor* out, const pd_tensor* workspace,
+                         int64_t nsplit, int64_t exact, hipStream_t stream, char* err, int errlen);
+
+/*
  * KV-cache writer and quantiser: the producer of the 520-byte rows the two operators read.
  * Replaces vLLM's cache update for int8 per-token-head KV, which the reference calls as
  * do_kv_cache_update(layer, key, value, kv_cache, slot_mapping)

@@ -255,7 +255,7 @@ int pth_dec_decode(const pd_tensor* q, const pd_tensor* key_cache, const pd_tens
 static int fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_tensor* value_cache,
                       const pd_tensor* block_table, const pd_tensor* seq_lens, double scale,
                       const pd_tensor* q_abs_offset, const pd_tensor* out, hipStream_t stream, char* err, int errlen,
-                      bool exact) {
+                      bool exact, int64_t nsplit = 1, const pd_tensor* workspace = nullptr) {
     if (!q || !key_cache || !value_cache || !block_table || !seq_lens || !q_abs_offset || !out)
         return fail(err, errlen, "null tensor descriptor");
     if (!(q->dtype == PD_DTYPE_FP32 && q->ndim == 4 && is_contig(q)))
@@ -299,6 +299,13 @@ static int fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_t
     if (!((reinterpret_cast<uintptr_t>(q->data) % 16) == 0 && (reinterpret_cast<uintptr_t>(out->data) % 16) == 0 &&
           out->strides[0] % 4 == 0 && out->strides[1] % 4 == 0 && out->strides[2] % 4 == 0))
         return fail(err, errlen, "q and out rows must be 16-byte aligned");
+    if (!(nsplit >= 1 && nsplit <= 64)) return fail(err, errlen, "nsplit must be in [1, 64]");
+    if (nsplit > 1) {
+        if (!(workspace && workspace->dtype == PD_DTYPE_FP32 && workspace->ndim == 1 && is_contig(workspace) &&
+              workspace->sizes[0] >= prefill_workspace_floats(B, Sq, Hq, nsplit) &&
+              (reinterpret_cast<uintptr_t>(workspace->data) % 16) == 0))
+            return fail(err, errlen, "workspace must be contiguous 16-byte aligned fp32 of B * Sq * Hq * nsplit * 258");
+    }
     if (B == 0 || Sq == 0) return 0;
     FaParams p;
     p.q = static_cast<const float*>(q->data);
@@ -329,6 +336,17 @@ static int fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_t
     const int64_t span = (key_cache->sizes[0] - 1) * key_cache->strides[0] + (bs - 1) * key_cache->strides[1] +
                          (Hkv - 1) * key_cache->strides[2] + 8;
     p.bt32 = span < ((int64_t)1 << 35);
+    p.nsplit = (int)nsplit;
+    p.part_o = nullptr;
+    p.part_m = nullptr;
+    p.part_l = nullptr;
+    if (nsplit > 1) {
+        float* ws = static_cast<float*>(const_cast<void*>(workspace->data));
+        const int64_t prow = B * Sq * Hq * nsplit;
+        p.part_o = ws;
+        p.part_m = ws + prow * kDim;
+        p.part_l = p.part_m + prow;
+    }
     const hipError_t e = launch_prefill(p, (int)B, (int)Hkv, stream, exact);
     if (e != hipSuccess) {
         char msg[256];
@@ -352,6 +370,14 @@ int pth_fa_forward_exact(const pd_tensor* q, const pd_tensor* key_cache, const p
                          int errlen) {
     return fa_forward(q, key_cache, value_cache, block_table, seq_lens, scale, q_abs_offset, out, stream, err, errlen,
                       true);
+}
+
+int pth_fa_forward_split(const pd_tensor* q, const pd_tensor* key_cache, const pd_tensor* value_cache,
+                         const pd_tensor* block_table, const pd_tensor* seq_lens, double scale,
+                         const pd_tensor* q_abs_offset, const pd_tensor* out, const pd_tensor* workspace,
+                         int64_t nsplit, int64_t exact, hipStream_t stream, char* err, int errlen) {
+    return fa_forward(q, key_cache, value_cache, block_table, seq_lens, scale, q_abs_offset, out, stream, err, errlen,
+                      exact != 0, nsplit, workspace);
 }
 
 int pth_cache_write(const pd_tensor* key, const pd_tensor* value, const pd_tensor* key_cache,

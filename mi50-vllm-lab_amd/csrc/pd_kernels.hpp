@@ -74,6 +74,13 @@ struct FaParams {
     int Sq, Hq, G, tok_per_wg, block_size, bs_shift;
     int bt32;                  // every K row lies within 2^35 bytes of the cache base
     float scale_log2;
+    // nsplit > 1: each query tile's visible key tiles are split into nsplit contiguous runs, one
+    // workgroup each, which store unnormalised partials (O, m, l) for every row; row r = (b * Sq +
+    // token) * Hq + head of split s at part_o[(r * nsplit + s) * 256], part_m / part_l[r * nsplit + s]
+    int nsplit;
+    float* part_o;
+    float* part_m;
+    float* part_l;
 };
 
 // KV-cache writer (pd_cache_write_kernel).
@@ -127,6 +134,10 @@ hipError_t scratch_address(void** out);
 // chunked prefill (pd_prefill.hip)
 // exact: K converted to fp16 without the widening bias and P' as fp16 hi + lo (pth_fa_forward_exact)
 hipError_t launch_prefill(const FaParams& p, int batch, int heads_kv, hipStream_t stream, bool exact);
+// workspace floats a split prefill needs: B * Sq * Hq rows x nsplit x (256 + 2)
+inline int64_t prefill_workspace_floats(int64_t B, int64_t Sq, int64_t Hq, int64_t nsplit) {
+    return B * Sq * Hq * nsplit * (kDim + 2);
+}
 
 // cache writer (pd_cache_write.hip); dtype is a PD_DTYPE_* code of key and value
 hipError_t launch_cache_write(const CacheWriteParams& p, int dtype, hipStream_t stream);

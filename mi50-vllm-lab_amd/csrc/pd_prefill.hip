@@ -76,7 +76,7 @@ __device__ __forceinline__ void wait_quarters(int later, bool tail) {
     }
 }
 
-template <bool kFast, bool kExact>
+template <bool kFast, bool kExact, bool kSplit>
 __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaParams a) {
     constexpr int kLdsRaw = 0;
     constexpr int kLdsH = kLdsRaw + kFaRaw * kSlot;
@@ -94,7 +94,11 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
     const unsigned lin = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
     const unsigned xcd = lin % 8u;
     const unsigned lidx = xcd * (nwg / 8u) + min(xcd, nwg % 8u) + lin / 8u;
-    const int qt = (int)(lidx % nx), g = (int)((lidx / nx) % ny), b = (int)(lidx / (nx * ny));
+    // x = split * (query tiles) + query tile: the query tiles of one split and kv head (which
+    // stream the same keys) stay neighbours in the XCD order
+    const int x = (int)(lidx % nx), g = (int)((lidx / nx) % ny), b = (int)(lidx / (nx * ny));
+    const int nqt = kSplit ? (int)nx / a.nsplit : (int)nx;
+    const int qt = kSplit ? x % nqt : x, split = kSplit ? x / nqt : 0;
     const int tid = threadIdx.x, l = tid & 63, lg = l >> 4, li = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = a.G;
@@ -106,6 +110,9 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
     const int hi = min(seq_len, qabs + tq0 + ntok);
     const int ntiles = hi > 0 ? (hi - 1) / kTile + 1 : 0;
     const int pmin = qabs + tq0;                       // smallest row position
+    // this workgroup's run of key tiles [t0, t1): all of them unless the keys are split
+    const int per = kSplit ? (ntiles + a.nsplit - 1) / a.nsplit : ntiles;
+    const int t0 = kSplit ? min(ntiles, split * per) : 0, t1 = kSplit ? min(ntiles, t0 + per) : ntiles;
 
     // ---- rows of this wave: row r = 48 w + 16 rb + li -> (token r / G, head r % G) ----
     half8_t qop[kFaRB][8];
@@ -157,12 +164,12 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
     {
         const int* bt_glob = a.block_table + (int64_t)b * a.bt_stride;
         if constexpr (kFast) {
-            const int nblk = 2 * ntiles;
+            const int nblk = 2 * (t1 - t0);  // the workgroup's tiles t0 + i / 2
             pt.in_lds = a.bt32 && nblk <= kFaBt;
             if (pt.in_lds) {
                 lds_int* dst = (lds_int*)(L + kLdsBt);
                 for (int i = tid; i < nblk; i += kFaWaves * 64) {
-                    const int kb = (i >> 1) * kTile;
+                    const int kb = (t0 + (i >> 1)) * kTile;
                     const int klast = min(kb + kTile - 1, hi - 1);
                     const int key0 = min(kb + 16 * (i & 1), klast) & ~15;
                     const int lb = key0 / a.block_size;
@@ -440,7 +447,7 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
         auto issue = [&](int n) __attribute__((always_inline)) {
             TileSrc src;
             if constexpr (kFast && kLds) {
-                const lds_int* e = pt.lds + 2 * n;
+                const lds_int* e = pt.lds + 2 * (n - t0);
                 const unsigned o0 = (unsigned)__builtin_amdgcn_readfirstlane(e[0]);
                 const unsigned o1 = (unsigned)__builtin_amdgcn_readfirstlane(e[1]);
                 src.base[0] = gbase + ((int64_t)o0 << 3);
@@ -472,20 +479,20 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
                 default: issue_quarter<kFast, 3>(a, src, dl, slot, l); break;
             }
         };
-        for (int n = 0; n < min(ntiles, kFaRaw); ++n) issue(n);
-        if (ntiles > 0) {
-            // tile 0 has landed; of tiles 1..3 at most 2 are left in flight (conservative)
-            wait_quarters(min(ntiles - 1, 2), tail_wave);
+        for (int n = t0; n < min(t1, t0 + kFaRaw); ++n) issue(n);
+        if (t1 > t0) {
+            // tile t0 has landed; of the next three at most 2 are left in flight (conservative)
+            wait_quarters(min(t1 - t0 - 1, 2), tail_wave);
             __syncthreads();
-            widen(0);
+            widen(t0);
         }
         // Iteration n: tile n + 1 has landed and every wave is done with iteration n - 1, so
         // fp16 buffer n & 1 holds tile n and raw slot n & 3 (widened in iteration n - 1) is free
         // for tile n + 4.
         auto arrive = [&](int n) __attribute__((always_inline)) {
-            if (n + 1 < ntiles) wait_quarters(min(2, ntiles - 2 - n), tail_wave);
+            if (n + 1 < t1) wait_quarters(min(2, t1 - 2 - n), tail_wave);
             __syncthreads();
-            if (n + kFaRaw < ntiles) issue(n + kFaRaw);
+            if (n + kFaRaw < t1) issue(n + kFaRaw);
         };
         float sv[kFaRB][8], vs[8];
         // The fast inner loops never rescale: O stays in the MFMA accumulators. When some row's
@@ -498,15 +505,16 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
                 tile_back(n, sv, vs);
             }
         };
-        run(std::false_type{}, 0, n_int);
-        run(std::true_type{}, n_int, ntiles);
+        run(std::false_type{}, t0, min(n_int, t1));
+        run(std::true_type{}, max(n_int, t0), t1);
     };
     if (pt.in_lds)
         tile_loop(std::true_type{});
     else
         tile_loop(std::false_type{});
 
-    // ---- normalise and store: out[b, tq0 + tok, g G + hh, :] ----
+    // ---- normalise and store: out[b, tq0 + tok, g G + hh, :]; with the keys split, the
+    //      unnormalised partial O, the running max m and the sum l of the row instead ----
 #pragma unroll
     for (int rb = 0; rb < kFaRB; ++rb) {
         const float l_row = xor_sum(xor_sum(l_run[rb], 16), 32);
@@ -516,31 +524,85 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
         if (rvalid[rb]) {
             const int r = 48 * w + 16 * rb + li;
             const int tok = r / G, hh = r - (r / G) * G;
-            float* orow = a.out + (int64_t)b * a.o_sb + (int64_t)(tq0 + tok) * a.o_st + (int64_t)(g * G + hh) * a.o_sh;
+            if constexpr (kSplit) {
+                const int64_t pr = (((int64_t)b * a.Sq + tq0 + tok) * a.Hq + g * G + hh) * a.nsplit + split;
+                float* prow = a.part_o + pr * kDim;
 #pragma unroll
-            for (int m = 0; m < 17; ++m) {
-                const int d0 = m < 16 ? 16 * m - 4 + 4 * lg : (lg == 2 ? 252 : -1);
-                if (d0 >= 0 && d0 < kDim) *reinterpret_cast<float4_t*>(orow + d0) = (oacc[rb][m] - corr) * inv;
+                for (int m = 0; m < 17; ++m) {
+                    const int d0 = m < 16 ? 16 * m - 4 + 4 * lg : (lg == 2 ? 252 : -1);
+                    if (d0 >= 0 && d0 < kDim) *reinterpret_cast<float4_t*>(prow + d0) = oacc[rb][m] - corr;
+                }
+                if (lg == 0) {
+                    a.part_m[pr] = m_run[rb];
+                    a.part_l[pr] = l_row;
+                }
+            } else {
+                float* orow = a.out + (int64_t)b * a.o_sb + (int64_t)(tq0 + tok) * a.o_st + (int64_t)(g * G + hh) * a.o_sh;
+#pragma unroll
+                for (int m = 0; m < 17; ++m) {
+                    const int d0 = m < 16 ? 16 * m - 4 + 4 * lg : (lg == 2 ? 252 : -1);
+                    if (d0 >= 0 && d0 < kDim) *reinterpret_cast<float4_t*>(orow + d0) = (oacc[rb][m] - corr) * inv;
+                }
             }
         }
     }
 }
 
+// Log-sum-exp merge of a split prefill's partials into out (fp32): one wave per row, lane l
+// owns dims 4 l .. 4 l + 3. M = max_s m_s, out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s,
+// and 0 for a row no split saw a key of.
+__global__ void __launch_bounds__(256) pd_prefill_combine_kernel(const FaParams a, int rows) {
+    const int r = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), l = threadIdx.x & 63;
+    if (r >= rows) return;
+    const int ns = a.nsplit;
+    const int64_t base = (int64_t)r * ns;
+    float M = kNegInf;
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, a.part_m[base + s]);
+    float4_t acc = (float4_t)0.f;
+    float L = 0.f;
+    if (M != kNegInf) {
+        for (int s = 0; s < ns; ++s) {
+            const float ms = a.part_m[base + s];
+            if (ms == kNegInf) continue;  // a split that saw no key of the row: its O is not used
+            const float wgt = exp2f(ms - M);
+            L += wgt * a.part_l[base + s];
+            acc += wgt * *reinterpret_cast<const float4_t*>(a.part_o + (base + s) * kDim + 4 * l);
+        }
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const int hd = r % a.Hq, tok = (r / a.Hq) % a.Sq, b = r / (a.Hq * a.Sq);
+    float* orow = a.out + (int64_t)b * a.o_sb + (int64_t)tok * a.o_st + (int64_t)hd * a.o_sh;
+    *reinterpret_cast<float4_t*>(orow + 4 * l) = acc * inv;
+}
+
 // ---------------------------------------------------------------------------------------
 // host side
 
-hipError_t launch_prefill(const FaParams& p, int batch, int heads_kv, hipStream_t stream, bool exact) {
-    const dim3 grid((p.Sq + p.tok_per_wg - 1) / p.tok_per_wg, heads_kv, batch);
+template <bool kSplit>
+static void launch_prefill_kernel(const FaParams& p, dim3 grid, hipStream_t stream, bool fast, bool exact) {
     const dim3 block(kFaWaves * 64);
-    const bool fast = fast_block_table(p.block_size, p.k_ss);
     if (fast && !exact)
-        hipLaunchKernelGGL((pd_prefill_kernel<true, false>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((pd_prefill_kernel<true, false, kSplit>), grid, block, 0, stream, p);
     else if (!exact)
-        hipLaunchKernelGGL((pd_prefill_kernel<false, false>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((pd_prefill_kernel<false, false, kSplit>), grid, block, 0, stream, p);
     else if (fast)
-        hipLaunchKernelGGL((pd_prefill_kernel<true, true>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((pd_prefill_kernel<true, true, kSplit>), grid, block, 0, stream, p);
     else
-        hipLaunchKernelGGL((pd_prefill_kernel<false, true>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((pd_prefill_kernel<false, true, kSplit>), grid, block, 0, stream, p);
+}
+
+hipError_t launch_prefill(const FaParams& p, int batch, int heads_kv, hipStream_t stream, bool exact) {
+    const dim3 grid(((p.Sq + p.tok_per_wg - 1) / p.tok_per_wg) * p.nsplit, heads_kv, batch);
+    const bool fast = fast_block_table(p.block_size, p.k_ss);
+    if (p.nsplit == 1) {
+        launch_prefill_kernel<false>(p, grid, stream, fast, exact);
+        return hipGetLastError();
+    }
+    launch_prefill_kernel<true>(p, grid, stream, fast, exact);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int rows = batch * p.Sq * p.Hq;
+    hipLaunchKernelGGL(pd_prefill_combine_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, p, rows);
     return hipGetLastError();
 }
 

@@ -50,6 +50,7 @@ EXPORTED_SYMBOLS = (
     "pth_dec_version",
     "pth_fa_forward",
     "pth_fa_forward_exact",
+    "pth_fa_forward_split",
     "pth_cache_write",
 )
 
@@ -108,6 +109,9 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.pth_fa_forward.restype = c_int
     lib.pth_fa_forward_exact.argtypes = lib.pth_fa_forward.argtypes
     lib.pth_fa_forward_exact.restype = c_int
+    lib.pth_fa_forward_split.argtypes = [tp] * 5 + [c_double, tp, tp, tp, ctypes.c_int64, ctypes.c_int64, vp,
+                                                    ctypes.c_char_p, c_int]
+    lib.pth_fa_forward_split.restype = c_int
     lib.pth_cache_write.argtypes = [tp] * 7 + [vp, ctypes.c_char_p, c_int]
     lib.pth_cache_write.restype = c_int
     lib.pth_dec_version.argtypes = []
@@ -169,9 +173,28 @@ def decode(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, 
         raise RuntimeError(err.value.decode())
 
 
+PREFILL_ROWS_PER_WORKGROUP = 192  # query rows (tokens x heads of one kv head) per prefill workgroup
+PREFILL_TARGET_WORKGROUPS = 256   # one per CU
+PREFILL_MAX_SPLITS = 64
+
+
+def prefill_splits(batch: int, sq: int, heads_q: int, heads_kv: int, max_keys: int) -> int:
+    """Key splits per query tile for a prefill launch: 1 when the query tiles alone give about
+    one workgroup per CU, else enough splits to reach that, at most 64 and with at least 8 key
+    tiles (256 keys) of max_keys per split. max_keys is a host-side upper bound on the keys a row
+    can see (the block table's width in keys); the device splits each row's actual keys evenly."""
+    g = max(1, heads_q // max(1, heads_kv))
+    qtiles = -(-sq // max(1, PREFILL_ROWS_PER_WORKGROUP // g))
+    wgs = qtiles * heads_kv * batch
+    if wgs <= 0 or wgs * 4 >= PREFILL_TARGET_WORKGROUPS * 3:
+        return 1
+    by_keys = max(1, -(-max_keys // 32) // 8)
+    return max(1, min(PREFILL_MAX_SPLITS, -(-PREFILL_TARGET_WORKGROUPS // wgs), by_keys))
+
+
 def forward_pth(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, block_table: torch.Tensor,
                 seq_lens: torch.Tensor, scale: float, q_abs_offset: torch.Tensor,
-                out: torch.Tensor | None = None, exact: bool = False) -> torch.Tensor:
+                out: torch.Tensor | None = None, exact: bool = False, nsplit: int | None = None) -> torch.Tensor:
     """Causal chunked prefill over the int8 per-token-head cache; returns fp32 [B, Sq, Hq, 256].
 
     q: fp32 [B, Hq, Sq, 256] contiguous; query token i of sequence b is at absolute position
@@ -180,6 +203,9 @@ def forward_pth(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Ten
     exact=True runs pth_fa_forward_exact, which has no counterpart in the reference: K without
     the widening bias and P' as fp16 hi + lo, for caches with very large scales (outlier
     tokens), at about twice the P.V matrix work.
+    nsplit: key splits per query tile (pth_fa_forward_split, no counterpart in the reference);
+    None picks them with prefill_splits (1 for chunks that fill the GPU), and a workspace for the
+    partials is taken from torch's allocator.
     """
     if not q.is_cuda:
         raise RuntimeError("q must be contiguous fp32 [B, Hq, Sq, D]")
@@ -189,11 +215,22 @@ def forward_pth(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Ten
     descs = [describe(t) for t in (q, key_cache, value_cache, block_table, seq_lens)]
     qa, od = describe(q_abs_offset), describe(out)
     err = ctypes.create_string_buffer(256)
+    if nsplit is None:
+        nsplit = prefill_splits(q.shape[0], q.shape[2], q.shape[1], key_cache.shape[2],
+                                block_table.shape[1] * key_cache.shape[1] if block_table.dim() == 2 else 0)
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
-        fn = lib.pth_fa_forward_exact if exact else lib.pth_fa_forward
-        rc = fn(*[ctypes.byref(x) for x in descs], float(scale), ctypes.byref(qa), ctypes.byref(od),
-                ctypes.c_void_p(stream), err, len(err))
+        if nsplit > 1:
+            ws = torch.empty((q.shape[0] * q.shape[2] * q.shape[1] * nsplit * (q.shape[3] + 2),), dtype=torch.float32,
+                             device=q.device)
+            wd = describe(ws)
+            rc = lib.pth_fa_forward_split(*[ctypes.byref(x) for x in descs], float(scale), ctypes.byref(qa),
+                                          ctypes.byref(od), ctypes.byref(wd), nsplit, 1 if exact else 0,
+                                          ctypes.c_void_p(stream), err, len(err))
+        else:
+            fn = lib.pth_fa_forward_exact if exact else lib.pth_fa_forward
+            rc = fn(*[ctypes.byref(x) for x in descs], float(scale), ctypes.byref(qa), ctypes.byref(od),
+                    ctypes.c_void_p(stream), err, len(err))
     if rc != 0:
         raise RuntimeError(err.value.decode())
     return out

@@ -287,6 +287,49 @@ def test_prefill_rejects_sizes_beyond_32_bits(lib, entry):
     assert rc == 1 and "below 2^31" in err.value.decode(), (rc, err.value)
 
 
+def test_prefill_split_count_policy():
+    """pth_dec.prefill_splits: no split once the query tiles give ~one workgroup per CU (a
+    2,048-token chunk of 24 q / 4 kv heads: 256), else enough splits to reach it, at most 64 and at
+    least 256 keys of the block table's width per split."""
+    ps = pth_dec.prefill_splits
+    assert ps(1, 2048, 24, 4, 63488) == 1
+    assert ps(1, 1024, 24, 4, 63488) == 2
+    assert ps(1, 512, 24, 4, 63488) == 4
+    assert ps(1, 64, 24, 4, 63488) == 32
+    assert ps(1, 16, 24, 4, 63488) == 64
+    assert ps(1, 64, 24, 4, 1000) == 4      # 32 key tiles: 8 per split at most 4 splits
+    assert ps(4, 2048, 24, 4, 63488) == 1
+    assert ps(1, 1, 8, 8, 100) == 1          # fewer than 8 key tiles: no split
+
+
+def test_prefill_split_validation_messages(lib):
+    """pth_fa_forward_split: the split count and the workspace are checked before anything runs."""
+    case = make(ctxs=[40, 9], qlens=[3, 3])
+    q = kvc.prefill_query(case)
+    B, hq, sq = q.shape[0], q.shape[1], q.shape[2]
+    need = B * sq * hq * 4 * 258
+    c = case.cache
+
+    def call(ws, nsplit):
+        out = torch.empty((B, sq, hq, 256))
+        descs = [pth_dec.describe(t) for t in (q, c.key_cache, c.value_cache, case.block_table, case.seq_lens)]
+        qa = pth_dec.describe(torch.tensor(case.ctxs, dtype=torch.int32))
+        od, wd = pth_dec.describe(out), pth_dec.describe(ws)
+        err = ctypes.create_string_buffer(256)
+        rc = lib.pth_fa_forward_split(*[ctypes.byref(x) for x in descs], case.scale, ctypes.byref(qa), ctypes.byref(od),
+                                      ctypes.byref(wd), nsplit, 0, None, err, len(err))
+        return rc, err.value.decode()
+
+    for ws, nsplit, msg in [(torch.empty(need), 0, "nsplit must be in [1, 64]"),
+                            (torch.empty(need), 65, "nsplit must be in [1, 64]"),
+                            (torch.empty(need - 1), 4, "workspace must be"),
+                            (torch.empty(need, dtype=torch.float64), 4, "workspace must be"),
+                            (torch.empty(2 * need)[::2], 4, "workspace must be"),
+                            (torch.empty(need + 1)[1:], 4, "workspace must be")]:
+        rc, text = call(ws, nsplit)
+        assert rc == 1 and msg in text, (nsplit, rc, text)
+
+
 @pytest.mark.parametrize("entry", PREFILL_ENTRIES)
 def test_prefill_empty_chunk_is_noop(lib, entry):
     case = make(ctxs=[40, 9], qlens=[3, 3])

@@ -238,6 +238,66 @@ def test_rows_that_see_one_or_two_keys():
     assert emax <= 2e-3 and emean <= 2e-4, (emax, emean)
 
 
+@pytest.mark.parametrize("nsplit", [2, 7, 64])
+def test_key_splits_match_the_unsplit_operator(nsplit):
+    """pth_fa_forward_split: each query tile's keys split over nsplit workgroups, merged by a second
+    kernel. The default numerics against the oracle (2e-3 / 2e-4; each split rounds P' to fp16
+    against its own running max, so the split and unsplit results differ by up to that
+    rounding), and the exact numerics against the unsplit exact operator, which leaves only the
+    order of the fp32 sums: the V products carry the widening bias, so those sums are ~1152 / |v|
+    times the result and their reordering moves it by up to ~1e-4 (a wrong merge moves it by O(1)).
+    Sequence 1 has fewer key tiles than 64 splits (empty splits) and rows before its first key
+    (written as 0)."""
+    ctxs, sq = [3000, 40, 517], 70
+    c = kvc.make_case(ctxs, [sq] * 3, num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=300 + nsplit)
+    q_abs = [3000, -20, 700]
+    say(f"prefill split {nsplit}")
+    d = c.to("cuda")
+    qd = kvc.prefill_query(d)
+    qa = torch.tensor(q_abs, dtype=torch.int32, device="cuda")
+    def run(n, exact):
+        return pth_dec.forward_pth(qd, d.cache.key_cache, d.cache.value_cache, d.block_table, d.seq_lens, d.scale, qa,
+                                   nsplit=n, exact=exact)
+
+    split = run(nsplit, False)
+    one_x, split_x = run(1, True), run(nsplit, True)
+    torch.cuda.synchronize()
+    ref, written = oracle_of(c, q_abs)
+    emax, emean = errors(split, ref, written)
+    diff = float((split_x - one_x).abs().max())
+    xmax, xmean = errors(split_x, ref, written)
+    say(f"  vs oracle: max-abs {emax:.2e} mean-abs {emean:.2e}; exact: {xmax:.2e} / {xmean:.2e}; "
+        f"exact split vs exact unsplit: max {diff:.2e}")
+    assert torch.isfinite(split).all() and torch.isfinite(split_x).all()
+    assert emax <= 2e-3 and emean <= 2e-4, (emax, emean)
+    assert xmax <= 2e-3 and xmean <= 2e-4, (xmax, xmean)
+    assert diff <= 2e-4, diff
+    assert (split.cpu().numpy()[~written] == 0).all() and (split_x.cpu().numpy()[~written] == 0).all()
+
+
+def test_key_splits_exact_and_short_chunk_over_long_context():
+    """The exact entry through the split path, and a 16-token chunk over 20,000 cached keys (the
+    case the split exists for: 4 workgroups without it), against the oracle."""
+    c = kvc.make_case([20000], [16], num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=321, outlier_frac=0.01)
+    q_abs = [20000]
+    say("prefill 16 tokens over 20000 keys, split, default and exact")
+    d = c.to("cuda")
+    qd = kvc.prefill_query(d)
+    qa = torch.tensor(q_abs, dtype=torch.int32, device="cuda")
+    assert pth_dec.prefill_splits(1, 16, HQ, HKV, d.block_table.shape[1] * 16) > 1
+    ref, written = oracle_of(c, q_abs)
+    mag, _ = oracle_of(abs_value_case(c), q_abs)
+    out = pth_dec.forward_pth(qd, d.cache.key_cache, d.cache.value_cache, d.block_table, d.seq_lens, d.scale, qa)
+    ex = pth_dec.forward_pth(qd, d.cache.key_cache, d.cache.value_cache, d.block_table, d.seq_lens, d.scale, qa,
+                             exact=True)
+    torch.cuda.synchronize()
+    err = np.abs(out.double().cpu().numpy() - ref)[written]
+    assert (err <= 2e-3 + 2.0 ** -11 * mag[written]).all()
+    emax, emean = errors(ex, ref, written)
+    say(f"  default max-abs {err.max():.2e}; exact max-abs {emax:.2e} mean-abs {emean:.2e}")
+    assert emax <= 2e-3 and emean <= 2e-4, (emax, emean)
+
+
 EXACT_CASES = [REF_CASES[i] for i in (0, 2, 3, 4, 6)]
 
 
