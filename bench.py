@@ -23,7 +23,7 @@ summaries committed under profiles/ for the same workload.
      quantisation: one call captured in a HIP graph and the graph replayed 1,000 times
   5  chunked prefill, a 2,048-token causal chunk over 61,440 cached tokens (63,488 keys), through
      pth_fa_forward and (under `exact`) pth_fa_forward_exact; `chunk64` is a 64-token chunk over
-     the same cache (keys split over 32 workgroups per query tile)
+     the same cache (keys split over 32 workgroups per query tile), `chunk2560` a 2,560-token one (4 splits)
   w  the KV-cache writer (pth_cache_write) on 4, 2,048 and 32,768 new tokens (fp16 K/V as
      strided views of a fused QKV buffer): µs per call, algorithmic GB/s, fraction of 8 TB/s
 Decode configs report µs per layer, algorithmic GB/s and the fraction of 8 TB/s; the prefill
@@ -603,12 +603,14 @@ def bench_prefill(torch, wl, pd, dev, stream, reps=20, exact_too=True):
         line["exact"] = {"entry": "pth_fa_forward_exact", "ms_per_chunk": round(mse, 4), "TFLOP_s": round(tfe, 1),
                          "frac": round(tfe / MFMA_FP16_PEAK_TFLOPS, 4)}
         line["chunk64"] = bench_short_prefill(torch, wl, pd, dev, stream, 64)
+        line["chunk2560"] = bench_short_prefill(torch, wl, pd, dev, stream, 2560, reps=10)
     return line
 
 
 def bench_short_prefill(torch, wl, pd, dev, stream, sq, reps=200):
-    """A short chunk (sq tokens) over the same 61,440 cached tokens: too few query tiles to fill the
-    GPU, so forward_pth splits each tile's keys (pth_fa_forward_split) and merges the splits."""
+    """A chunk of sq tokens over the same 61,440 cached tokens, with the key split that forward_pth
+    picks (pth_fa_forward_split): 64 tokens give too few query tiles to fill the GPU, 2,560 give
+    320 workgroups, which unsplit would run as one full round and one part-filled round."""
     ctx = PREFILL_CTX
     case = wl.make_case([ctx], [sq], num_q_heads=24, num_kv_heads=4, block_size=16, seed=1005)
     flops = wl.prefill_flops([ctx + sq], [ctx], sq, 24)
@@ -618,20 +620,25 @@ def bench_short_prefill(torch, wl, pd, dev, stream, sq, reps=200):
     qa = torch.tensor([ctx], dtype=torch.int32, device=dev)
     out = torch.empty((1, sq, 24, 256), dtype=torch.float32, device=dev)
     nsplit = pd.prefill_splits(1, sq, 24, 4, d.block_table.shape[1] * 16)
-    ops = [lambda c=c: pd.forward_pth(q, c.key_cache, c.value_cache, d.block_table, d.seq_lens, d.scale, qa, out=out)
-           for c in caches]
-    with torch.cuda.stream(stream):
-        for o in ops:
-            o()
-    torch.cuda.synchronize()
-    g = graph_of(torch, stream, ops)
-    with torch.cuda.stream(stream):
-        g.replay()
-        ms = time_replays(torch, g, reps // 2, stream) / reps
+
+    def timed(ns, n):
+        ops = [lambda c=c: pd.forward_pth(q, c.key_cache, c.value_cache, d.block_table, d.seq_lens, d.scale, qa,
+                                          out=out, nsplit=ns) for c in caches]
+        with torch.cuda.stream(stream):
+            for o in ops:
+                o()
+        torch.cuda.synchronize()
+        g = graph_of(torch, stream, ops)
+        with torch.cuda.stream(stream):
+            g.replay()
+            return time_replays(torch, g, n // 2, stream) / n
+
+    ms = timed(nsplit, reps)
+    ms1 = timed(1, max(2, reps // 20))
     kv = (ctx + sq) * 4 * 520
     return {"tokens": sq, "nsplit": nsplit, "ms_per_chunk": round(ms, 4),
             "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1), "KV_GB_s": round(kv / (ms * 1e-3) / 1e9, 1),
-            "timed": f"{reps // 2} replays of a 2-call graph over 2 cache copies"}
+            "ms_unsplit": round(ms1, 4), "timed": f"{reps // 2} replays of a 2-call graph over 2 cache copies"}
 
 
 KVW_TOKENS = (4, 2048, 32768)

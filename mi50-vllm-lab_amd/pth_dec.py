@@ -174,22 +174,54 @@ def decode(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, 
 
 
 PREFILL_ROWS_PER_WORKGROUP = 192  # query rows (tokens x heads of one kv head) per prefill workgroup
-PREFILL_TARGET_WORKGROUPS = 256   # one per CU
+PREFILL_CUS = 256                 # workgroups that run at once: one per CU (the LDS takes the CU)
 PREFILL_MAX_SPLITS = 64
+PREFILL_MIN_TILES_PER_SPLIT = 8   # 256 keys
+# makespan model of a prefill launch on MI355X (fit to graph-replayed chunks of 16..6,144 tokens
+# over 8k..61k cached tokens): a workgroup costs ~16 us plus ~1.62 us per 32-key tile; a split
+# launch adds ~0.6 us per MB of partials (stored, then merged) and ~5 us for the merge launch
+PREFILL_US_PER_TILE = 1.62
+PREFILL_US_PER_WORKGROUP = 16.0
+PREFILL_US_PER_PARTIAL_MB = 0.6
+PREFILL_US_MERGE_LAUNCH = 5.0
+PREFILL_MAX_WORKSPACE = 1 << 30   # bytes of partials a split launch may take
+
+
+def prefill_cost_us(batch: int, sq: int, heads_q: int, heads_kv: int, max_keys: int, nsplit: int) -> float:
+    """Modelled time of one prefill launch with nsplit key splits per query tile: the workgroups
+    run in ceil(workgroups / 256) rounds, each as long as the longest split (every row taken to
+    see max_keys keys), plus the partials' store and merge when nsplit > 1."""
+    g = max(1, heads_q // max(1, heads_kv))
+    qtiles = -(-sq // max(1, PREFILL_ROWS_PER_WORKGROUP // g))
+    wgs = qtiles * heads_kv * batch * nsplit
+    tiles = -(-max(0, max_keys) // 32)
+    rounds = -(-wgs // PREFILL_CUS)
+    t = rounds * (-(-tiles // nsplit) * PREFILL_US_PER_TILE + PREFILL_US_PER_WORKGROUP)
+    if nsplit > 1:
+        t += PREFILL_US_MERGE_LAUNCH + PREFILL_US_PER_PARTIAL_MB * batch * sq * heads_q * nsplit * 1032 / 1e6
+    return t
 
 
 def prefill_splits(batch: int, sq: int, heads_q: int, heads_kv: int, max_keys: int) -> int:
-    """Key splits per query tile for a prefill launch: 1 when the query tiles alone give about
-    one workgroup per CU, else enough splits to reach that, at most 64 and with at least 8 key
-    tiles (256 keys) of max_keys per split. max_keys is a host-side upper bound on the keys a row
-    can see (the block table's width in keys); the device splits each row's actual keys evenly."""
-    g = max(1, heads_q // max(1, heads_kv))
-    qtiles = -(-sq // max(1, PREFILL_ROWS_PER_WORKGROUP // g))
-    wgs = qtiles * heads_kv * batch
-    if wgs <= 0 or wgs * 4 >= PREFILL_TARGET_WORKGROUPS * 3:
+    """Key splits per query tile for a prefill launch: the count in 1..64 that minimises
+    prefill_cost_us, with at least 8 key tiles (256 keys) of max_keys per split and at most 1 GiB
+    of partials. Splitting pays where the query tiles alone leave CUs idle: short chunks (a 64-token
+    chunk over 61k keys: 32 splits) and chunks whose workgroups end in a part-filled round (2,560
+    tokens, 320 workgroups: 4 splits run them in 5 full rounds of a quarter of the keys instead of
+    2 rounds of all of them). max_keys is a host-side upper bound on the keys a row can see (the
+    block table's width in keys); the device splits each row's actual keys evenly."""
+    if batch <= 0 or sq <= 0 or heads_q <= 0 or heads_kv <= 0:
         return 1
-    by_keys = max(1, -(-max_keys // 32) // 8)
-    return max(1, min(PREFILL_MAX_SPLITS, -(-PREFILL_TARGET_WORKGROUPS // wgs), by_keys))
+    tiles = -(-max(0, max_keys) // 32)
+    top = max(1, min(PREFILL_MAX_SPLITS, tiles // PREFILL_MIN_TILES_PER_SPLIT))
+    best, best_t = 1, prefill_cost_us(batch, sq, heads_q, heads_kv, max_keys, 1)
+    for ns in range(2, top + 1):
+        if batch * sq * heads_q * ns * 1032 > PREFILL_MAX_WORKSPACE:
+            break
+        t = prefill_cost_us(batch, sq, heads_q, heads_kv, max_keys, ns)
+        if t < best_t:
+            best, best_t = ns, t
+    return best
 
 
 def forward_pth(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, block_table: torch.Tensor,

@@ -288,18 +288,30 @@ def test_prefill_rejects_sizes_beyond_32_bits(lib, entry):
 
 
 def test_prefill_split_count_policy():
-    """pth_dec.prefill_splits: no split once the query tiles give ~one workgroup per CU (a
-    2,048-token chunk of 24 q / 4 kv heads: 256), else enough splits to reach it, at most 64 and at
-    least 256 keys of the block table's width per split."""
+    """pth_dec.prefill_splits picks the count that the makespan model rates fastest. Each pin below
+    is the count that was fastest on an MI355X (graph replays, 24 q / 4 kv heads over 61,440
+    cached tokens unless noted: 2,560 tokens 6.72 ms unsplit, 4.12 at 4 splits; 3,072 tokens 6.63
+    unsplit, 4.88 at 2; 3,072 over 8,192 cached 1.19 unsplit, 0.88 at 2; 6,144 tokens 10.02
+    unsplit, 9.97 at 2; 64 tokens 0.155 ms at 32 splits against 0.185-0.24 at 16, 24, 48 and 64)."""
     ps = pth_dec.prefill_splits
     assert ps(1, 2048, 24, 4, 63488) == 1
     assert ps(1, 1024, 24, 4, 63488) == 2
     assert ps(1, 512, 24, 4, 63488) == 4
     assert ps(1, 64, 24, 4, 63488) == 32
     assert ps(1, 16, 24, 4, 63488) == 64
+    assert ps(1, 2560, 24, 4, 64000) == 4    # 320 workgroups: 5 full rounds of quarter runs
+    assert ps(1, 3072, 24, 4, 64512) == 2    # 384 workgroups: 3 rounds of half runs
+    assert ps(1, 3072, 24, 4, 11264) == 2
+    assert ps(1, 6144, 24, 4, 67584) == 1    # 768 workgroups: 3 full rounds already
     assert ps(1, 64, 24, 4, 1000) == 4      # 32 key tiles: 8 per split at most 4 splits
     assert ps(4, 2048, 24, 4, 63488) == 1
     assert ps(1, 1, 8, 8, 100) == 1          # fewer than 8 key tiles: no split
+    assert ps(0, 64, 24, 4, 63488) == 1
+    # the partials stay within 1 GiB: 16,384 tokens x 24 heads x 1,032 B is 406 MB per split
+    assert ps(1, 16384, 24, 4, 1 << 20) <= 2
+    # the model itself: a part-filled last round costs a whole round
+    c = pth_dec.prefill_cost_us
+    assert c(1, 2560, 24, 4, 63488, 1) == 2 * c(1, 2048, 24, 4, 63488, 1)
 
 
 def test_prefill_split_validation_messages(lib):
