@@ -29,6 +29,16 @@ def make_inputs(T, hkv, dtype, seed):
     k[0, 0] = torch.randint(-254, 255, (256,), generator=g).float() * 0.0625
     k[0, 0, 0] = 127 * 0.125
     v[1 % T, 0] = 0.0                       # all-zero row
+    # near-ties (float32 inputs): within 4 ulps of (m + 0.5) * scale for every m, where only a
+    # correctly rounded x / scale gives the oracle's byte
+    if T > 2:
+        sc = np.float32(np.float32(38.1) / np.float32(127))
+        near = ((np.arange(-126, 126, dtype=np.float32) + np.float32(0.5)) * sc).astype(np.float32)
+        bits = near.view(np.int32) + np.where(near < 0, -1, 1) * np.resize(np.array([-4, -1, 1, 3]), near.size)
+        row = np.zeros(256, np.float32)
+        row[:near.size] = bits.astype(np.int32).view(np.float32)
+        row[255] = 38.1
+        k[2, 1] = torch.from_numpy(row)
     return k.to(dtype), v.to(dtype)
 
 

@@ -80,3 +80,4 @@ def test_write_rows_slot_semantics(layout):
     for slot in (3, 40, 95):
         mask[slot // 16, slot % 16] = False
     assert torch.equal(cache.kv.transpose(1, 2)[mask], before.transpose(1, 2)[mask])
+
