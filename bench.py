@@ -379,6 +379,9 @@ def main():
     ap.add_argument("--profile-prefill", type=int, default=0, metavar="N",
                     help="run N config-5 prefill chunks (alternating two cache copies) and nothing else, for "
                          "rocprofv3")
+    ap.add_argument("--profile-prefill-chunk", type=int, default=0, metavar="TOKENS",
+                    help="with --profile-prefill N: a chunk of TOKENS over the same 61,440 cached tokens through "
+                         "forward_pth's key split (N + 4 calls, then 6 unsplit ones), instead of the 2,048-token chunk")
     ap.add_argument("--profile-kvwrite", type=int, default=0, metavar="N",
                     help="run N KV-cache writer calls on the largest writer workload and nothing else, for "
                          "rocprofv3")
@@ -428,6 +431,13 @@ def main():
         calibration_copies(torch, dev)
         print(json.dumps({"profile_kvwrite": True, "tokens": KVW_TOKENS[-1], "us_per_call": res["us_per_call"],
                           "GB_s": res["GB_s"], "calib_copies": CALIB_COPIES, "calib_bytes": CALIB_BYTES}))
+        return
+
+    if args.profile_prefill and args.profile_prefill_chunk:
+        n = 2 * max(1, args.profile_prefill // 2)
+        res = bench_short_prefill(torch, wl, pd, dev, stream, args.profile_prefill_chunk, reps=n)
+        print(json.dumps({"profile_prefill": True, "tokens": res["tokens"], "nsplit": res["nsplit"],
+                          "split_calls": n + 4, "ms_per_chunk": res["ms_per_chunk"], "ms_unsplit": res["ms_unsplit"]}))
         return
 
     if args.profile_prefill:

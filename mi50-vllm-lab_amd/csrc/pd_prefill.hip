@@ -550,23 +550,35 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
 
 // Log-sum-exp merge of a split prefill's partials into out (fp32): one wave per row, lane l
 // owns dims 4 l .. 4 l + 3. M = max_s m_s, out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s,
-// and 0 for a row no split saw a key of.
+// and 0 for a row no split saw a key of. Lane s reads split s's m and l (nsplit <= 64), the wave
+// reduces M and L, and the O rows are loaded eight splits at a time before any is used, so a
+// row costs about nsplit / 8 memory round trips. A split that saw no key of the row leaves its O
+// unwritten: it is loaded (the workspace holds it) but excluded by a select, not a product.
 __global__ void __launch_bounds__(256) pd_prefill_combine_kernel(const FaParams a, int rows) {
+    constexpr int kBatch = 8;
     const int r = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), l = threadIdx.x & 63;
     if (r >= rows) return;
     const int ns = a.nsplit;
     const int64_t base = (int64_t)r * ns;
-    float M = kNegInf;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, a.part_m[base + s]);
+    const float m_mine = l < ns ? a.part_m[base + l] : kNegInf;
+    const float l_mine = l < ns ? a.part_l[base + l] : 0.f;
+    float M = m_mine;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    const float w_mine = m_mine != kNegInf ? exp2f(m_mine - M) : 0.f;
+    float L = w_mine * l_mine;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o, 64);
     float4_t acc = (float4_t)0.f;
-    float L = 0.f;
-    if (M != kNegInf) {
-        for (int s = 0; s < ns; ++s) {
-            const float ms = a.part_m[base + s];
-            if (ms == kNegInf) continue;  // a split that saw no key of the row: its O is not used
-            const float wgt = exp2f(ms - M);
-            L += wgt * a.part_l[base + s];
-            acc += wgt * *reinterpret_cast<const float4_t*>(a.part_o + (base + s) * kDim + 4 * l);
+    const float4_t* po = reinterpret_cast<const float4_t*>(a.part_o + base * kDim) + l;
+    for (int s0 = 0; s0 < ns; s0 += kBatch) {
+        float4_t o[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) o[i] = s0 + i < ns ? po[(int64_t)(s0 + i) * (kDim / 4)] : (float4_t)0.f;
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const float wi = __shfl(w_mine, min(s0 + i, 63), 64);
+            acc += (s0 + i < ns && wi != 0.f) ? wi * o[i] : (float4_t)0.f;
         }
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
