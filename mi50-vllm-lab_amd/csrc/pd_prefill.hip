@@ -552,8 +552,8 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
 // owns dims 4 l .. 4 l + 3. M = max_s m_s, out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s,
 // and 0 for a row no split saw a key of. Lane s reads split s's m and l (nsplit <= 64), the wave
 // reduces M and L, and the O rows are loaded eight splits at a time before any is used, so a
-// row costs about nsplit / 8 memory round trips. A split that saw no key of the row leaves its O
-// unwritten: it is loaded (the workspace holds it) but excluded by a select, not a product.
+// row costs about nsplit / 8 memory round trips. A split that saw no key of the row (m = -inf)
+// is excluded by a select, not a product, so whatever its O holds cannot reach the output.
 __global__ void __launch_bounds__(256) pd_prefill_combine_kernel(const FaParams a, int rows) {
     constexpr int kBatch = 8;
     const int r = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), l = threadIdx.x & 63;

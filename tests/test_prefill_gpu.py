@@ -36,11 +36,11 @@ def oracle_of(c, q_abs, rows=None):
                              c.cache.v_scale, c.block_table, c.seq_lens, c.scale, torch.tensor(q_abs), rows)
 
 
-def gpu_prefill(d, q_abs, exact=False):
+def gpu_prefill(d, q_abs, exact=False, nsplit=None):
     q = kvc.prefill_query(d)
     out = torch.full((q.shape[0], q.shape[2], q.shape[1], 256), float("nan"), dtype=torch.float32, device="cuda")
     pth_dec.forward_pth(q, d.cache.key_cache, d.cache.value_cache, d.block_table, d.seq_lens, d.scale,
-                        torch.tensor(q_abs, dtype=torch.int32, device="cuda"), out=out, exact=exact)
+                        torch.tensor(q_abs, dtype=torch.int32, device="cuda"), out=out, exact=exact, nsplit=nsplit)
     torch.cuda.synchronize()
     return out
 
@@ -358,11 +358,17 @@ def test_physical_layout_bit_exact(bs):
     assert torch.equal(oa.view(torch.int32), ob.view(torch.int32))
 
 
-def test_hip_graph_capture_and_replay():
+@pytest.mark.parametrize("nsplit", [1, None])
+def test_hip_graph_capture_and_replay(nsplit):
+    """Captured once, replayed three times, each replay bit-equal to the eager call: the unsplit
+    launch, and (nsplit None: forward_pth's pick, 8 splits here) the split launch with its merge
+    and the workspace taken from the graph's pool."""
     c = kvc.make_case([5000], [256], num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=31).to("cuda")
+    if nsplit is None:
+        assert pth_dec.prefill_splits(1, 256, HQ, HKV, c.block_table.shape[1] * 16) > 1
     q = kvc.prefill_query(c)
     qa = torch.tensor([5000], dtype=torch.int32, device="cuda")
-    ref = gpu_prefill(c, [5000])
+    ref = gpu_prefill(c, [5000], nsplit=nsplit)
     out = torch.zeros_like(ref)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -370,7 +376,7 @@ def test_hip_graph_capture_and_replay():
     with torch.cuda.stream(s):
         with torch.cuda.graph(g, stream=s):
             pth_dec.forward_pth(q, c.cache.key_cache, c.cache.value_cache, c.block_table, c.seq_lens, c.scale, qa,
-                                out=out)
+                                out=out, nsplit=nsplit)
     torch.cuda.current_stream().wait_stream(s)
     for i in range(3):
         out.fill_(float("nan"))
