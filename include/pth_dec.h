@@ -173,11 +173,11 @@ int pth_fa_forward_exact(const pd_tensor* q, const pd_tensor* key_cache, const p
  * No counterpart in the reference. pth_fa_forward (exact != 0: pth_fa_forward_exact) with each
  * query tile's keys split over nsplit workgroups, for chunks too short to fill the GPU (a
  * workgroup takes 192 query rows of one kv head, so a 64-token chunk of 24 q / 4 kv heads
- * launches 8 of them per split). Each split stores unnormalised partials in the caller's
+ * launches 8 of them per split) or whose workgroups end in a part-filled round. Each split stores unnormalised partials in the caller's
  * workspace, and a second kernel merges them into out.
  *   workspace  fp32, contiguous, 16-byte aligned, at least B * Sq * Hq * nsplit * 258 floats
  *              (ignored when nsplit == 1)
- *   nsplit     1..64
+ *   nsplit     1..64; when above 1, B * Sq * Hq must be below 2^31
  * Other arguments, checks, errors and return codes are those of pth_fa_forward. The results
  * equal pth_fa_forward's within rounding (the partial sums are merged in another order).
  */

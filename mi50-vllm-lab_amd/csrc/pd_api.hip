@@ -300,6 +300,9 @@ static int fa_forward(const pd_tensor* q, const pd_tensor* key_cache, const pd_t
           out->strides[0] % 4 == 0 && out->strides[1] % 4 == 0 && out->strides[2] % 4 == 0))
         return fail(err, errlen, "q and out rows must be 16-byte aligned");
     if (!(nsplit >= 1 && nsplit <= 64)) return fail(err, errlen, "nsplit must be in [1, 64]");
+    // the merge numbers rows (b, token, head) in 32 bits; B, Sq < 2^31 keep B * Sq within int64
+    if (nsplit > 1 && Hq > 0 && B * Sq > INT32_MAX / Hq)
+        return fail(err, errlen, "a split prefill takes at most 2^31 - 1 (token, head) rows");
     if (nsplit > 1) {
         if (!(workspace && workspace->dtype == PD_DTYPE_FP32 && workspace->ndim == 1 && is_contig(workspace) &&
               workspace->sizes[0] >= prefill_workspace_floats(B, Sq, Hq, nsplit) &&

@@ -342,6 +342,32 @@ def test_prefill_split_validation_messages(lib):
         assert rc == 1 and msg in text, (nsplit, rc, text)
 
 
+def test_prefill_split_rejects_more_than_2_31_rows(lib):
+    """pth_fa_forward_split numbers its (token, head) rows in 32 bits: a chunk of 2^27 tokens x 24
+    heads is refused (descriptors claiming that size over small real buffers, never read)."""
+    case = make(ctxs=[40, 9], qlens=[3, 3])
+    q = kvc.prefill_query(case)
+    B, hq = q.shape[0], q.shape[1]
+    big = 1 << 27
+    qd = pth_dec.describe(q)
+    qd.sizes[2] = big
+    for i, st in enumerate((hq * big * 256, big * 256, 256, 1)):
+        qd.strides[i] = st
+    od = pth_dec.describe(torch.empty((B, 3, hq, 256)))
+    od.sizes[1] = big
+    for i, st in enumerate((big * hq * 256, hq * 256, 256, 1)):
+        od.strides[i] = st
+    wd = pth_dec.describe(torch.empty(16))
+    wd.sizes[0] = B * big * hq * 2 * 258
+    c = case.cache
+    descs = [pth_dec.describe(t) for t in (c.key_cache, c.value_cache, case.block_table, case.seq_lens)]
+    qa = pth_dec.describe(torch.tensor(case.ctxs, dtype=torch.int32))
+    err = ctypes.create_string_buffer(256)
+    rc = lib.pth_fa_forward_split(ctypes.byref(qd), *[ctypes.byref(x) for x in descs], case.scale, ctypes.byref(qa),
+                                  ctypes.byref(od), ctypes.byref(wd), 2, 0, None, err, len(err))
+    assert rc == 1 and "at most 2^31 - 1 (token, head) rows" in err.value.decode(), (rc, err.value)
+
+
 @pytest.mark.parametrize("entry", PREFILL_ENTRIES)
 def test_prefill_empty_chunk_is_noop(lib, entry):
     case = make(ctxs=[40, 9], qlens=[3, 3])
