@@ -12,7 +12,8 @@ Every output and partial buffer has sentinel guards on both sides that must stay
 the inputs must be unchanged afterwards.
 
 Prefill cases draw group sizes, batches, chunk lengths, block sizes, layouts and chunk offsets
-(rows before the first key, chunks ending the sequence or past it). KV-cache writer cases draw
+(rows before the first key, chunks ending the sequence or past it), and for the key-split
+entry a split count from 2 to 64 and the numerics. KV-cache writer cases draw
 token and head counts, block sizes, layouts, dtypes, padding slots and row magnitudes over many
 decades, with key and value as strided views into one fused QKV buffer (vLLM's form), and must
 match the oracle's cache bytes exactly.
@@ -174,9 +175,21 @@ def test_prefill_random_exact(i):
     run_prefill_case(i, exact=True)
 
 
-def run_prefill_case(i, exact):
+N_PREFILL_SPLIT = 12
+
+
+@pytest.mark.parametrize("i", range(60, 60 + N_PREFILL_SPLIT))
+def test_prefill_random_split(i):
+    """pth_fa_forward_split on cases drawn like the default's (other seeds), with a split count and
+    the numerics drawn too: 2..64 splits over random batches, contexts, chunk offsets, GQA groups,
+    block sizes and layouts, to the same bar."""
+    rng = np.random.default_rng(7700 + i)
+    run_prefill_case(i, exact=bool(rng.integers(0, 2)), nsplit=int(rng.choice([2, 3, 5, 8, 17, 40, 64])))
+
+
+def run_prefill_case(i, exact, nsplit=None):
     p = draw_prefill(i)
-    say(f"prefill sweep {i} exact={exact}: {p}")
+    say(f"prefill sweep {i} exact={exact} nsplit={nsplit}: {p}")
     c = kvc.make_case(p["ctxs"], [p["sq"]] * len(p["ctxs"]), num_q_heads=p["hq"], num_kv_heads=p["hkv"],
                       block_size=p["bs"], layout=p["layout"], seed=p["seed"], kv_mode=p["kv_mode"])
     ref, written = orc.paged_prefill(kvc.prefill_query(c), c.cache.key_cache, c.cache.value_cache, c.cache.k_scale,
@@ -188,7 +201,8 @@ def run_prefill_case(i, exact):
     before = fingerprint(*inputs)
     wo, out = guarded((q.shape[0], q.shape[2], q.shape[1], 256), torch.float32, float("nan"))
     pth_dec.forward_pth(q, d.cache.key_cache, d.cache.value_cache, d.block_table, d.seq_lens, d.scale,
-                        torch.tensor(p["q_abs"], dtype=torch.int32, device="cuda"), out=out, exact=exact)
+                        torch.tensor(p["q_abs"], dtype=torch.int32, device="cuda"), out=out, exact=exact,
+                        nsplit=nsplit)
     torch.cuda.synchronize()
     assert guards_intact(wo), "a write outside the output"
     assert fingerprint(*inputs) == before, "an input was written"
