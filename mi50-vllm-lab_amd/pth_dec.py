@@ -226,7 +226,8 @@ def prefill_splits(batch: int, sq: int, heads_q: int, heads_kv: int, max_keys: i
 
 def forward_pth(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, block_table: torch.Tensor,
                 seq_lens: torch.Tensor, scale: float, q_abs_offset: torch.Tensor,
-                out: torch.Tensor | None = None, exact: bool = False, nsplit: int | None = None) -> torch.Tensor:
+                out: torch.Tensor | None = None, exact: bool = False, nsplit: int | None = None,
+                max_keys: int | None = None) -> torch.Tensor:
     """Causal chunked prefill over the int8 per-token-head cache; returns fp32 [B, Sq, Hq, 256].
 
     q: fp32 [B, Hq, Sq, 256] contiguous; query token i of sequence b is at absolute position
@@ -238,6 +239,9 @@ def forward_pth(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Ten
     nsplit: key splits per query tile (pth_fa_forward_split, no counterpart in the reference);
     None picks them with prefill_splits (1 for chunks that fill the GPU), and a workspace for the
     partials is taken from torch's allocator.
+    max_keys: a host-side bound on the keys any row of the batch sees (the longest seq_len), used
+    only to pick nsplit; None takes the block table's width in keys, which for a table sized to
+    the model's maximum length plans every chunk for the longest context.
     """
     if not q.is_cuda:
         raise RuntimeError("q must be contiguous fp32 [B, Hq, Sq, D]")
@@ -248,8 +252,9 @@ def forward_pth(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Ten
     qa, od = describe(q_abs_offset), describe(out)
     err = ctypes.create_string_buffer(256)
     if nsplit is None:
-        nsplit = prefill_splits(q.shape[0], q.shape[2], q.shape[1], key_cache.shape[2],
-                                block_table.shape[1] * key_cache.shape[1] if block_table.dim() == 2 else 0)
+        if max_keys is None:
+            max_keys = block_table.shape[1] * key_cache.shape[1] if block_table.dim() == 2 else 0
+        nsplit = prefill_splits(q.shape[0], q.shape[2], q.shape[1], key_cache.shape[2], int(max_keys))
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
         if nsplit > 1:

@@ -267,12 +267,24 @@ class Gfx950Int8Attention:
                                      output[:qsl[p]], max_q_prefix, meta,
                                      None if meta.seq_lens_cpu is None else meta.seq_lens_cpu[:p])):
             triton_fallback(0, qsl[p], 0, p, max_q_prefix)
+        # The split count of each prefill is planned for the keys its sequence sees: the host length
+        # when it is known and no graph is being captured (vLLM's block table is as wide as the
+        # model's maximum length, so the table alone would plan every chunk for the longest context),
+        # else the batch's max_seq_len, else the table width.
+        lens_host = meta.seq_lens_cpu if meta.seq_lens_cpu is not None and not _capturing(query.device) else None
         for i in range(p, n):
             start, nq = qsl[i], qsl[i + 1] - qsl[i]
             q = query[start:start + nq].transpose(0, 1).unsqueeze(0).float().contiguous()  # [1, Hq, nq, D]
             seq_len = meta.seq_lens[i:i + 1]
+            if lens_host is not None:
+                max_keys = int(lens_host[i])
+            elif meta.max_seq_len > 0 and not _capturing(query.device):
+                max_keys = int(meta.max_seq_len)
+            else:
+                max_keys = None
             out = self.pth_fa.forward_pth(q, key_cache, value_cache, meta.block_table[i:i + 1], seq_len, self.scale,
-                                          seq_len - nq, **({"exact": True} if PTH_FA_EXACT else {}))
+                                          seq_len - nq, max_keys=max_keys,
+                                          **({"exact": True} if PTH_FA_EXACT else {}))
             output[start:start + nq] = out[0].to(output.dtype)
         return True
 

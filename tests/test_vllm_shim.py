@@ -26,9 +26,10 @@ class FakeOps:
         self.calls.append(("decode", q.shape[0], num_seqs, qmax, nsplit, window, bt.shape[0]))
         out.fill_(1.0)
 
-    def forward_pth(self, q, kc, vc, bt, sl, scale, q_abs, exact=False):
+    def forward_pth(self, q, kc, vc, bt, sl, scale, q_abs, exact=False, max_keys=None):
         self.calls.append(("prefill", tuple(q.shape), int(sl[0]), int(q_abs[0]), q.dtype))
         self.exact = getattr(self, "exact", []) + [exact]
+        self.max_keys = getattr(self, "max_keys", []) + [max_keys]
         return torch.full((1, q.shape[2], q.shape[1], q.shape[3]), 2.0)
 
 
@@ -204,6 +205,46 @@ def test_prefill_suffix_with_decode_prefix(ops):
     assert pre == [("prefill", (1, 24, 100, 256), 1100, 1000, torch.float32),
                    ("prefill", (1, 24, 70, 256), 70, 0, torch.float32)]
     assert (out[:2] == 1).all() and (out[2:] == 2).all()
+
+
+@pytest.mark.parametrize("nq,ctx", [(64, 0), (700, 0), (2560, 0), (5824, 0), (2048, 61440)])
+def test_prefill_split_planned_for_the_host_length(ops, monkeypatch, nq, ctx):
+    """vLLM's block table is as wide as max_model_len. The shim passes each sequence's host length
+    to forward_pth, so a short prompt under a 131,072-key table is planned for its own keys
+    (a fresh prompt up to ~5.8k tokens fills the GPU unsplit), not for the table's width; the
+    table width is used only while a graph is being captured or without host lengths."""
+    from mi50_vllm_lab_amd import pth_dec as pdm
+    a = impl()
+    q, out, kc = tensors(nq)
+    m = meta([nq], [ctx + nq])
+    m.block_table = torch.zeros((1, 131072 // 16), dtype=torch.int32)
+    m.seq_lens_cpu = [ctx + nq]
+    assert a.route(q, kc, kc, None, None, m, out, nq, nq, lambda *x: pytest.fail("fallback"))
+    assert ops.max_keys[-1] == ctx + nq
+    planned = pdm.prefill_splits(1, nq, 24, 4, ops.max_keys[-1])
+    if ctx == 0 and nq >= 700:
+        assert planned == 1
+    # what the table width alone would plan: every chunk as if over 131,072 keys
+    wide = pdm.prefill_splits(1, nq, 24, 4, m.block_table.shape[1] * kc.shape[1])
+    assert planned <= wide
+    m.seq_lens_cpu = None  # no host lengths: the batch's max_seq_len
+    assert a.route(q, kc, kc, None, None, m, out, nq, nq, lambda *x: pytest.fail("fallback"))
+    assert ops.max_keys[-1] == ctx + nq
+    monkeypatch.setattr(shim, "_capturing", lambda device: True)  # capture: the table width
+    m.seq_lens_cpu = [ctx + nq]
+    assert a.route(q, kc, kc, None, None, m, out, nq, nq, lambda *x: pytest.fail("fallback"))
+    assert ops.max_keys[-1] is None
+
+
+def test_prefill_split_plan_of_a_short_prompt_under_a_wide_table():
+    """The planning numbers behind the test above: under a 131,072-key table a 700-token fresh
+    prompt was planned with 11 splits (a 191 MB workspace) and a 64-token one with 32; planned
+    for their own keys both run unsplit."""
+    from mi50_vllm_lab_amd import pth_dec as pdm
+    assert pdm.prefill_splits(1, 700, 24, 4, 131072) > 1
+    assert pdm.prefill_splits(1, 700, 24, 4, 700) == 1
+    assert pdm.prefill_splits(1, 64, 24, 4, 131072) > 1
+    assert pdm.prefill_splits(1, 64, 24, 4, 64) == 1
 
 
 @pytest.mark.parametrize("exact", [False, True])
