@@ -37,7 +37,8 @@
 //     in fp16 has the range of p * v_scale * 256 with p <= 1. Masked weights are chosen by
 //     select, so a NaN scale on a masked row cannot leak in.
 //   O^T += V^T P^T: ds_read_b64_tr_b8 hands each lane 8 keys of one V column (A operand,
-//     16 dims x 32 keys); P^T never leaves registers: the S^T accumulator layout (lane = query
+//     16 dims x 32 keys, widened exactly like K); P^T never leaves registers: the S^T
+//     accumulator layout (lane = query
 //     row, 4 keys per 16-key block) is the B-operand layout once the MFMA's key order is chosen
 //     to match. Dim block j < 16 reads row bytes [256 + 16 j, 272 + 16 j) (dims 16 j - 4 ..),
 //     block 16 the tail bytes (dims 244..255); lanes outside [0, 256) are discarded.
@@ -141,14 +142,11 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     constexpr int kLdsBt = kLdsStats + 2 * kWaves * NRB * 16 * 4;
     constexpr int kLdsRaw = kLdsBt + (kEarly ? kBtEarly : kBtCache) * 8;
     constexpr int kLdsQ = kLdsRaw + (kEarly ? kBtRaw * 4 : 0);
-    // the merge's table of V widening biases reuses the Q region (or follows the block table)
     // (three row blocks: Q is staged in the V images of slot 1 of waves 0..2 instead, 16 rows
     // each; those slots receive their V copies only after Q is in registers)
     constexpr bool kQInSlots = NRB >= 3;
     constexpr int kQBytes = kEarly && !kQInSlots ? 16 * NRB * 2 * kDim : 0;
-    constexpr int kMergeCBytes = kWaves * NRB * 16 * 4;
-    constexpr int kLdsMergeC = kLdsQ;
-    constexpr int kLdsBytes = kLdsQ + (kQBytes > kMergeCBytes ? kQBytes : kMergeCBytes);
+    constexpr int kLdsBytes = kLdsQ + kQBytes;
     static_assert(2 * 17 * 1024 <= kWaveLds && kWaveLds % 16 == 0,
                   "two row blocks of accumulator blocks fit the slots of their wave");
     static_assert(kLdsBytes <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
@@ -259,7 +257,7 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
 
     // Running state per row block: max (log2 units), this lane's partial sum of p, and O^T in
     // 17 blocks of 16 "dims" (block m < 16: dims 16 m - 4 .. 16 m + 11; block 16: dims 244..255,
-    // then 1152 * sum P' in lane group 3, the widening bias of V to remove at the end).
+    // then 4 rows from the v_scale bytes in lane group 3, never stored).
     float m_run[NRB], l_run[NRB];
     float4_t oacc[NRB][17];
 #pragma unroll
@@ -537,7 +535,8 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
 
     // ---- p = 2^sv; P' = p * v_scale * 16 as two fp16 parts (hi + lo, ~22 significant bits: a
     //      single fp16 would put 2^-12 relative error on every term, too much next to outlier V
-    //      rows); then O^T += V^T hi^T + V^T lo^T for every row block ----
+    //      rows); then O^T += V^T hi^T + V^T lo^T for every row block, V widened exactly (no
+    //      bias: the fp32 accumulators hold only the products' own sums) ----
     auto tile_values = [&](const TileOps& o, const float (&sv)[NRB][8], bool interior) __attribute__((always_inline)) {
         float vsc[8];
 #pragma unroll
@@ -565,7 +564,7 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         }
 #pragma unroll
         for (int m = 0; m < 17; ++m) {
-            const half8_t vf = widen_i8x8((unsigned)o.v[m].x, (unsigned)o.v[m].y);
+            const half8_t vf = widen_i8x8_exact((unsigned)o.v[m].x, (unsigned)o.v[m].y);
 #pragma unroll
             for (int rb = 0; rb < NRB; ++rb)
                 oacc[rb][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, phi[rb], oacc[rb][m], 0, 0, 0);
@@ -576,15 +575,13 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     };
 
     // ---- every operand of a tile from its slot into registers, so the slot can be refilled
-    //      before the tile is computed: v_scale of this lane's keys (then the v_scale words of the
-    //      slot are cleared: that MFMA output row of the tail block becomes 1152 * sum P'), the K
-    //      operand, k_scale, and the 17 transposed V reads ----
+    //      before the tile is computed: v_scale of this lane's keys, the K operand, k_scale, and
+    //      the 17 transposed V reads ----
     auto read_ops = [&](lds_u8* T, TileOps& o) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int j = 0; j < 4; ++j) o.vs[4 * u + j] = *(const lds_float*)(T + vso[u] + 16 * j);
-        if (l < 32) *(lds_float*)(T + kImgT + 16 * l + 12) = 0.f;
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
@@ -702,22 +699,19 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     {
         // Each wave stores its accumulators as they are (a 1 KiB block per accumulator and row
         // block, straight from the AGPRs: no vector ALU work) into its own slots as soon as its
-        // tiles are done, with its per-row max, sum and V widening bias; then thread (row, 32
+        // tiles are done, with its per-row max and sum; then thread (row, 32
         // dims) derives the wave factors of its row, sums the four waves' blocks with them and
         // writes the partial row. Row blocks go through the slots two at a time (kRawRounds
         // rounds).
         constexpr int kRawRounds = (NRB + 1) / 2;
         float* wm = reinterpret_cast<float*>(lds + kLdsStats);  // [wave][NRB][16] running max
         float* wl = wm + kWaves * NRB * 16;                     // [wave][NRB][16] row sum of p
-        float* wc = reinterpret_cast<float*>(lds + kLdsMergeC);  // [wave][NRB][16] 1152 sum P'
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) {
             const float l_row = xor_sum(xor_sum(l_run[rb], 16), 32);
-            const float cr = __shfl(oacc[rb][16].x, 48 + li, 64);  // 1152 * sum of the row's P'
             if (lg == 0) {
                 wm[(w * NRB + rb) * 16 + li] = m_run[rb];
                 wl[(w * NRB + rb) * 16 + li] = l_row;
-                wc[(w * NRB + rb) * 16 + li] = cr;
             }
         }
         const unsigned raw = lds_base + (unsigned)(w * kWaveLds + 16 * l);  // this wave's slots
@@ -741,21 +735,20 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
                 __syncthreads();
             }
             // thread: row 32 rd + (lane & 31), wave w's two 32-dim parts. Row factors: M =
-            // max_w m_w, e_w = 2^(m_w - M), O = sum_w e_w O_w / 16 - sum_w e_w C_w / 16, L =
-            // sum_w e_w l_w. Dims d of an accumulator block: block m < 16 holds 16 m - 4 + 4 lg
+            // max_w m_w, e_w = 2^(m_w - M), O = sum_w e_w O_w / 16, L = sum_w e_w l_w. Dims d of
+            // an accumulator block: block m < 16 holds 16 m - 4 + 4 lg
             // .. + 3 in lane group lg, block 16 holds 252..255 in lane group 2
             const int row = 32 * rd + (l & 31), part = 2 * w + (l >> 5);
             if (row < R) {
                 float M = kNegInf;
 #pragma unroll
                 for (int v = 0; v < kWaves; ++v) M = fmaxf(M, wm[v * NRB * 16 + row]);
-                float f[kWaves], C = 0.f, Lr = 0.f;
+                float f[kWaves], Lr = 0.f;
 #pragma unroll
                 for (int v = 0; v < kWaves; ++v) {
                     const float mw = wm[v * NRB * 16 + row];
                     const float e = mw == kNegInf ? 0.f : exp2f(mw - M);
                     f[v] = e * (1.0f / kPScale);
-                    C += f[v] * wc[v * NRB * 16 + row];
                     Lr += e * wl[v * NRB * 16 + row];
                 }
                 const int64_t pr = prow(row);
@@ -772,9 +765,9 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
                     const int m = d < 252 ? (d + 4) >> 4 : 16;
                     const int glg = d < 252 ? ((d + 4) >> 2) & 3 : 2;
                     const int blk = (rbl * 17 + m) * 64 + 16 * glg + (row & 15);
-                    float4_t acc = (float4_t)(-C);
+                    float4_t acc = rawp[blk] * f[0];
 #pragma unroll
-                    for (int v = 0; v < kWaves; ++v) acc += rawp[v * (kWaveLds / 16) + blk] * f[v];
+                    for (int v = 1; v < kWaves; ++v) acc += rawp[v * (kWaveLds / 16) + blk] * f[v];
                     *reinterpret_cast<float4_t*>(dst + d) = acc;
                 }
             }

@@ -10,9 +10,11 @@
 //                registers, K and V operands read from the fp16 buffer.
 // One barrier per tile orders the three stages. There is no split: each row is normalised in
 // registers and stored once. Q arrives as fp32 and is rounded to fp16 for the MFMA.
-// kExact (pth_fa_forward_exact) gives the decode kernel's numerics: K is widened without the
-// bias (so the fp32 score accumulators hold only partial scores) and P' enters the P.V products
-// as fp16 hi + lo, which doubles them.
+// kExact (pth_fa_forward_exact) gives the decode kernel's numerics: K and V are widened without
+// the bias (so the fp32 accumulators hold only the products' own sums) and P' enters the P.V
+// products as fp16 hi + lo, which doubles them. The default instance keeps the bias in K and V
+// and removes it per row (sum_d q_d (k_d + 1152) - 1152 sum_d q_d, sum_k P'_k (v_k + 1152) -
+// 1152 sum_k P'_k).
 #include <type_traits>
 
 #include "pd_tile.hpp"
@@ -278,13 +280,21 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
                 kf = hh == 0 ? widen_i8x8(r.kr[u].x, r.kr[u].y) : widen_i8x8(r.kr[u].z, r.kr[u].w);
             *(lds_half8*)(H + ((2 * w + hh) * 2 + u) * 1024 + 16 * l) = kf;
         } else if (j < 8) {
+            // kExact: V widened exactly (no bias), so the fp32 P.V accumulators hold only the
+            // products' own sums; else with the bias, removed per row at the end
+            const int2_t vr = r.vr[j - 4];
             *(lds_half8*)(H + kFaHK + (w + 4 * (j - 4)) * 1024 + 16 * l) =
-                widen_i8x8((unsigned)r.vr[j - 4].x, (unsigned)r.vr[j - 4].y);
+                kExact ? widen_i8x8_exact((unsigned)vr.x, (unsigned)vr.y) : widen_i8x8((unsigned)vr.x, (unsigned)vr.y);
         } else if (j == 8) {
-            // rows 12..15 of the tail block are the v_scale bytes: widened from 0 they are
-            // exactly 1152, so O^T rows 252..255 of that block accumulate 1152 * sum of P'
-            const int2_t vt = li >= 12 ? int2_t{0, 0} : r.vr[4];
-            *(lds_half8*)(H + kFaHK + 16 * 1024 + 16 * l) = widen_i8x8((unsigned)vt.x, (unsigned)vt.y);
+            // rows 12..15 of the tail block are the v_scale bytes. kExact: the O^T rows they feed
+            // (lane group 3 of accumulator block 16) are never stored. Else they are widened from
+            // 0 to exactly 1152, so those rows accumulate 1152 * sum of P', the bias to remove
+            if constexpr (kExact) {
+                *(lds_half8*)(H + kFaHK + 16 * 1024 + 16 * l) = widen_i8x8_exact((unsigned)r.vr[4].x, (unsigned)r.vr[4].y);
+            } else {
+                const int2_t vt = li >= 12 ? int2_t{0, 0} : r.vr[4];
+                *(lds_half8*)(H + kFaHK + 16 * 1024 + 16 * l) = widen_i8x8((unsigned)vt.x, (unsigned)vt.y);
+            }
         } else {
             // k_scale * scale * log2(e) [32] then v_scale [32]; keys past seq_len may hold garbage
             // scales (even NaN): v_scale 0 makes their P' 0
@@ -519,7 +529,8 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
     for (int rb = 0; rb < kFaRB; ++rb) {
         const float l_row = xor_sum(xor_sum(l_run[rb], 16), 32);
         const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
-        const float corr = __shfl(oacc[rb][16].x, 48 + li, 64);  // 1152 * sum of the row's P'
+        // the V widening bias of the row, 1152 * sum of its P' (0 when V is widened exactly)
+        const float corr = kExact ? 0.f : __shfl(oacc[rb][16].x, 48 + li, 64);
 
         if (rvalid[rb]) {
             const int r = 48 * w + 16 * rb + li;

@@ -55,8 +55,8 @@ constexpr int kSlot = kImgT + 1024;
 
 // 8 signed bytes b (two dwords, byte 0 first) -> 8 fp16 holding b + 1152, exact: the bit
 // pattern 0x6400 | (b ^ 0x80) encodes 1024 + (b + 128). The constant 1152 is not subtracted
-// here; the kernel removes it once per row instead: O = sum_k P'_k (v_k + 1152) - 1152 sum_k P'_k
-// in both kernels, and S = sum_d q_d (k_d + 1152) - 1152 sum_d q_d in the prefill.
+// here; the default prefill removes it once per row instead: O = sum_k P'_k (v_k + 1152) -
+// 1152 sum_k P'_k and S = sum_d q_d (k_d + 1152) - 1152 sum_d q_d.
 constexpr float kWidenBias = 1152.0f;
 __device__ __forceinline__ half8_t widen_i8x8(unsigned w0, unsigned w1) {
     const unsigned u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;  // b + 128 as unsigned bytes
@@ -72,8 +72,9 @@ __device__ __forceinline__ half8_t widen_i8x8(unsigned w0, unsigned w1) {
 // 8 signed bytes b (as widen_i8x8) -> 8 fp16 holding b itself, exact: each byte is sign-extended
 // and converted by an SDWA v_cvt_f16_i16 straight into its half of the destination. One
 // instruction per value against 0.75 for widen_i8x8, with no bias left in the operand, so the
-// products of the decode's scores accumulate without the 1152 sum_d q_d that the fp32
-// accumulator would otherwise carry (and round) along with them.
+// products accumulate without the 1152 sum_d q_d (scores) or 1152 sum_k P'_k (values) that the
+// fp32 accumulator would otherwise carry (and round) along with them. The decode widens K and V
+// this way, and so does the exact prefill.
 __device__ __forceinline__ half8_t widen_i8x8_exact(unsigned w0, unsigned w1) {
     uint4_t h;
     asm("v_cvt_f16_i16_sdwa %0, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"

@@ -244,8 +244,10 @@ def test_key_splits_match_the_unsplit_operator(nsplit):
     kernel. The default numerics against the oracle (2e-3 / 2e-4; each split rounds P' to fp16
     against its own running max, so the split and unsplit results differ by up to that
     rounding), and the exact numerics against the unsplit exact operator, which leaves only the
-    order of the fp32 sums: the V products carry the widening bias, so those sums are ~1152 / |v|
-    times the result and their reordering moves it by up to ~1e-4 (a wrong merge moves it by O(1)).
+    order of the fp32 sums: K and V are widened exactly, so those sums are of the result's own
+    magnitude and their reordering moves it by at most 3.1e-5 here (1.6e-5 / 3.1e-5 / 2.6e-5 at
+    2 / 7 / 64 splits; bound 5e-5). With V widened as v + 1152 the same sums were ~1152 / |v|
+    times the result and moved it by up to 6.3e-4. A wrong merge moves it by O(1).
     Sequence 1 has fewer key tiles than 64 splits (empty splits) and rows before its first key
     (written as 0)."""
     ctxs, sq = [3000, 40, 517], 70
@@ -271,7 +273,7 @@ def test_key_splits_match_the_unsplit_operator(nsplit):
     assert torch.isfinite(split).all() and torch.isfinite(split_x).all()
     assert emax <= 2e-3 and emean <= 2e-4, (emax, emean)
     assert xmax <= 2e-3 and xmean <= 2e-4, (xmax, xmean)
-    assert diff <= 2e-4, diff
+    assert diff <= 5e-5, diff
     assert (split.cpu().numpy()[~written] == 0).all() and (split_x.cpu().numpy()[~written] == 0).all()
 
 
@@ -333,14 +335,18 @@ def test_exact_batches_and_group_sizes(bs, layout, hq, hkv):
     assert (out.cpu().numpy()[~written] == 0).all()
 
 
-@pytest.mark.parametrize("bs", [16, 8])
-def test_page_table_beyond_lds(bs):
-    # more 16-key blocks (bs 16: 6,252) or pages (bs 8: 12,500) than the workgroup's LDS table
-    # holds (6,144 entries), so the tile addresses come from the global block table
+@pytest.mark.parametrize("bs,nsplit", [(16, 1), (8, 1), (16, None), (8, None)])
+def test_page_table_beyond_lds(bs, nsplit):
+    """nsplit 1: a workgroup streams more 16-key blocks (bs 16: 6,252) or pages (bs 8: 12,500)
+    than its LDS table holds (6,144 entries), so the tile addresses come from the global block
+    table: the 16-key-block path at bs 16, the per-row path at bs 8. nsplit None (forward_pth's
+    pick, 32 splits of ~98 tiles): each split's slice fits the LDS table again."""
     ctx = 100000
     c = kvc.make_case([ctx], [40], num_q_heads=HQ, num_kv_heads=HKV, block_size=bs, seed=21 + bs)
-    say(f"prefill global page table bs={bs}")
-    out = gpu_prefill(c.to("cuda"), [ctx])
+    if nsplit == 1:  # more entries than the LDS table's 6,144: 16-key blocks at bs 16, pages at bs 8
+        assert -(-(ctx + 40) // 16) > 6144 and -(-(ctx + 40) // bs) > 6144
+    say(f"prefill global page table bs={bs} nsplit={nsplit}")
+    out = gpu_prefill(c.to("cuda"), [ctx], nsplit=nsplit)
     ref, written = oracle_of(c, [ctx], [0, 13, 39])
     emax, emean = errors(out, ref, written)
     say(f"  max-abs {emax:.2e} mean-abs {emean:.2e}")
