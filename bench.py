@@ -389,6 +389,9 @@ def main():
                     help="no GPU work: turn a rocprofv3 --pmc run of --profile-only with the counters in "
                          "bench.COUNTERS into instruction mix and MFMA utilisation, written to --counters-out")
     ap.add_argument("--counters-out", default=os.path.join(PROFILES, "pd_partial_mtp61k_counters.json"))
+    ap.add_argument("--prefill-grid", metavar="HQ,HKV,BS",
+                    help="the reference's prefill sweep: one 2,048-token chunk over 0/16k/64k/128k cached tokens "
+                         "(one JSON line per cell), e.g. 12,2,1584 (one TP=2 rank, as the reference) or 24,4,16")
     ap.add_argument("--grid", metavar="HQ,HKV,BS",
                     help="only the reference's decode speed grid (B x q_len x ctx) at HQ q heads, HKV kv heads "
                          "and block size BS, one JSON line per cell")
@@ -420,6 +423,11 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream()
+
+    if args.prefill_grid:
+        hq, hkv, bs = (int(x) for x in args.prefill_grid.split(","))
+        bench_prefill_grid(torch, wl, pd, dev, stream, hq, hkv, bs)
+        return
 
     if args.grid:
         hq, hkv, bs = (int(x) for x in args.grid.split(","))
@@ -494,7 +502,9 @@ def main():
             continue
         c = decode_case(wl, n)
         ns = shim.decode_splits(NSEG, c.window, 4, c.num_seqs, dev, c.seq_lens.tolist(), c.qmax)
-        copies = {1: 32, 3: 2, 4: 1}[n]
+        # enough cache copies that the visible pages in rotation exceed the 256 MB Infinity Cache
+        # (config 1: 32 x 8.5 MB; config 3: 16 x 17.1 MB); config 4 reads 416 MB per call
+        copies = {1: 32, 3: 16, 4: 1}[n]
         db = DecodeBench(torch, wl, pd, dev, c, copies, ns)
         with torch.cuda.stream(stream):
             for i in range(copies):
@@ -505,7 +515,7 @@ def main():
             reps, per = 1000, 1
         else:
             g = graph_of(torch, stream, [db.op(i) for i in range(copies)])
-            reps, per = (30 if n == 1 else 250), copies
+            reps, per = (30 if n == 1 else 60), copies
         with torch.cuda.stream(stream):
             for _ in range(max(1, reps // 10)):
                 g.replay()
@@ -513,7 +523,9 @@ def main():
         us = ms * 1e3 / (reps * per)
         line = decode_line(us, db)
         line["workload"] = DESCRIPTIONS[n]
-        line["timed"] = f"{reps} replays of a {per}-call graph" + ("" if n == 4 else f" over {copies} cache copies")
+        line["timed"] = f"{reps} replays of a {per}-call graph" + (
+            "" if n == 4 else f" over {copies} cache copies ({copies * wl.visible_kv_bytes(c) / 1e6:.0f} MB of "
+                              f"visible pages in rotation)")
         configs[str(n)] = line
         del db, g
         torch.cuda.empty_cache()
@@ -649,6 +661,55 @@ def bench_short_prefill(torch, wl, pd, dev, stream, sq, reps=200):
     return {"tokens": sq, "nsplit": nsplit, "ms_per_chunk": round(ms, 4),
             "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1), "KV_GB_s": round(kv / (ms * 1e-3) / 1e9, 1),
             "ms_unsplit": round(ms1, 4), "timed": f"{reps // 2} replays of a 2-call graph over 2 cache copies"}
+
+
+PREFILL_GRID_CTX = (0, 16384, 65536, 131072)
+# kernels/fa_pth/test_pth.py:113-125 on MI50, one TP=2 rank (12 q / 2 kv heads, block size 1,584):
+# ms per 2,048-token chunk over each cached context (docs/logs/test_pth.log:11-14)
+PREFILL_GRID_MI50_MS = {0: 7.2, 16384: 98.2, 65536: 376.2, 131072: 747.4}
+
+
+def bench_prefill_grid(torch, wl, pd, dev, stream, hq, hkv, block_size, reps=20):
+    """The reference's prefill speed sweep (kernels/fa_pth/test_pth.py:113-125): one 2,048-token
+    causal chunk on top of 0 / 16k / 64k / 128k cached tokens, through forward_pth with the key
+    split it picks for the chunk's keys (max_keys = ctx + 2,048), timed as graph replays over two
+    cache copies. FLOPs as test_pth.py:118, 4 D Hq (2048 ctx + 2048 * 2049 / 2). One JSON line per
+    cell, with the unsplit time as well."""
+    sq = PREFILL_CHUNK
+    for ctx in PREFILL_GRID_CTX:
+        case = wl.make_case([ctx], [sq], num_q_heads=hq, num_kv_heads=hkv, block_size=block_size, seed=1500 + ctx % 997)
+        d = case.to(dev)
+        caches = [d.cache, wl.clone_cache(d.cache)]
+        q = wl.prefill_query(d)
+        qa = torch.tensor([ctx], dtype=torch.int32, device=dev)
+        out = torch.empty((1, sq, hq, 256), dtype=torch.float32, device=dev)
+        flops = 4 * 256 * hq * (sq * ctx + sq * (sq + 1) // 2)
+        pick = pd.prefill_splits(1, sq, hq, hkv, ctx + sq, block_size)
+
+        def timed(ns, n):
+            ops = [lambda c=c: pd.forward_pth(q, c.key_cache, c.value_cache, d.block_table, d.seq_lens, d.scale, qa,
+                                              out=out, nsplit=ns) for c in caches]
+            with torch.cuda.stream(stream):
+                for o in ops:
+                    o()
+            torch.cuda.synchronize()
+            g = graph_of(torch, stream, ops)
+            with torch.cuda.stream(stream):
+                g.replay()
+                return time_replays(torch, g, n // 2, stream) / n
+
+        n = reps if ctx <= 65536 else max(4, reps // 2)
+        ms = timed(pick, n)
+        ms1 = ms if pick == 1 else timed(1, n)
+        mi50 = PREFILL_GRID_MI50_MS[ctx]
+        print(json.dumps({"prefill_grid": True, "heads_q": hq, "heads_kv": hkv, "block_size": block_size,
+                          "ctx": ctx, "chunk": sq, "nsplit_pick": pick, "ms_per_chunk": round(ms, 4),
+                          "ms_unsplit": round(ms1, 4), "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1),
+                          "frac": round(flops / (ms * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4), "flops": flops,
+                          "mi50_rank_ms": mi50, "timed": f"{n // 2} replays of a 2-call graph over 2 cache copies"}),
+              flush=True)
+        del caches, d, case, q, out
+        torch.cuda.empty_cache()
 
 
 KVW_TOKENS = (4, 2048, 32768)

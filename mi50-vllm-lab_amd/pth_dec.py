@@ -185,9 +185,16 @@ PREFILL_US_PER_WORKGROUP = 16.0
 PREFILL_US_PER_PARTIAL_MB = 0.6
 PREFILL_US_MERGE_LAUNCH = 5.0
 PREFILL_MAX_WORKSPACE = 1 << 30   # bytes of partials a split launch may take
+# A workgroup keeps its block-table slice in LDS when it has at most 6,144 entries (16-key blocks
+# when the block size is a multiple of 16, else pages); past that its tile addresses come from
+# scalar loads of the global table, ~15 % more per tile (2,048 tokens over 131k keys, 24 q / 4 kv
+# heads, bs 16: 7.79 ms unsplit, 1.87 against 1.63 us per tile)
+PREFILL_LDS_TABLE = 6144
+PREFILL_GLOBAL_TABLE_FACTOR = 1.15
 
 
-def prefill_cost_us(batch: int, sq: int, heads_q: int, heads_kv: int, max_keys: int, nsplit: int) -> float:
+def prefill_cost_us(batch: int, sq: int, heads_q: int, heads_kv: int, max_keys: int, nsplit: int,
+                    block_size: int = 16) -> float:
     """Modelled time of one prefill launch with nsplit key splits per query tile: the workgroups
     run in ceil(workgroups / 256) rounds, each as long as the longest split (every row taken to
     see max_keys keys), plus the partials' store and merge when nsplit > 1."""
@@ -196,29 +203,36 @@ def prefill_cost_us(batch: int, sq: int, heads_q: int, heads_kv: int, max_keys: 
     wgs = qtiles * heads_kv * batch * nsplit
     tiles = -(-max(0, max_keys) // 32)
     rounds = -(-wgs // PREFILL_CUS)
-    t = rounds * (-(-tiles // nsplit) * PREFILL_US_PER_TILE + PREFILL_US_PER_WORKGROUP)
+    per_split = -(-tiles // nsplit)
+    if block_size % 16 == 0:
+        in_lds = 2 * per_split <= PREFILL_LDS_TABLE
+    else:  # the page table of [0, seq_len), whatever the split
+        in_lds = -(-max(0, max_keys) // max(1, block_size)) <= PREFILL_LDS_TABLE
+    tile_us = PREFILL_US_PER_TILE * (1.0 if in_lds else PREFILL_GLOBAL_TABLE_FACTOR)
+    t = rounds * (per_split * tile_us + PREFILL_US_PER_WORKGROUP)
     if nsplit > 1:
         t += PREFILL_US_MERGE_LAUNCH + PREFILL_US_PER_PARTIAL_MB * batch * sq * heads_q * nsplit * 1032 / 1e6
     return t
 
 
-def prefill_splits(batch: int, sq: int, heads_q: int, heads_kv: int, max_keys: int) -> int:
+def prefill_splits(batch: int, sq: int, heads_q: int, heads_kv: int, max_keys: int, block_size: int = 16) -> int:
     """Key splits per query tile for a prefill launch: the count in 1..64 that minimises
     prefill_cost_us, with at least 8 key tiles (256 keys) of max_keys per split and at most 1 GiB
     of partials. Splitting pays where the query tiles alone leave CUs idle: short chunks (a 64-token
     chunk over 61k keys: 32 splits) and chunks whose workgroups end in a part-filled round (2,560
     tokens, 320 workgroups: 4 splits run them in 5 full rounds of a quarter of the keys instead of
-    2 rounds of all of them). max_keys is a host-side upper bound on the keys a row can see (the
-    block table's width in keys); the device splits each row's actual keys evenly."""
+    2 rounds of all of them), and long contexts whose key tiles overflow a workgroup's LDS block
+    table (2,048 tokens over 131k keys at bs 16: 2 splits). max_keys is a host-side upper bound on
+    the keys a row can see; the device splits each row's actual keys evenly."""
     if batch <= 0 or sq <= 0 or heads_q <= 0 or heads_kv <= 0:
         return 1
     tiles = -(-max(0, max_keys) // 32)
     top = max(1, min(PREFILL_MAX_SPLITS, tiles // PREFILL_MIN_TILES_PER_SPLIT))
-    best, best_t = 1, prefill_cost_us(batch, sq, heads_q, heads_kv, max_keys, 1)
+    best, best_t = 1, prefill_cost_us(batch, sq, heads_q, heads_kv, max_keys, 1, block_size)
     for ns in range(2, top + 1):
         if batch * sq * heads_q * ns * 1032 > PREFILL_MAX_WORKSPACE:
             break
-        t = prefill_cost_us(batch, sq, heads_q, heads_kv, max_keys, ns)
+        t = prefill_cost_us(batch, sq, heads_q, heads_kv, max_keys, ns, block_size)
         if t < best_t:
             best, best_t = ns, t
     return best
@@ -254,7 +268,8 @@ def forward_pth(q: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Ten
     if nsplit is None:
         if max_keys is None:
             max_keys = block_table.shape[1] * key_cache.shape[1] if block_table.dim() == 2 else 0
-        nsplit = prefill_splits(q.shape[0], q.shape[2], q.shape[1], key_cache.shape[2], int(max_keys))
+        nsplit = prefill_splits(q.shape[0], q.shape[2], q.shape[1], key_cache.shape[2], int(max_keys),
+                                key_cache.shape[1] if key_cache.dim() == 4 else 16)
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
         if nsplit > 1:

@@ -312,6 +312,17 @@ def test_prefill_split_count_policy():
     # the model itself: a part-filled last round costs a whole round
     c = pth_dec.prefill_cost_us
     assert c(1, 2560, 24, 4, 63488, 1) == 2 * c(1, 2048, 24, 4, 63488, 1)
+    # 2,048 tokens over 131,072 cached (4,160 key tiles, 8,320 16-key blocks: more than a
+    # workgroup's 6,144-entry LDS table): 7.76 ms unsplit, 6.69 ms at 2 splits (each split's
+    # table fits); over 65,536 cached it fits unsplit (3.43 ms)
+    assert ps(1, 2048, 24, 4, 133120) == 2
+    assert ps(1, 2048, 24, 4, 67584) == 1
+    assert c(1, 2048, 24, 4, 133120, 1) > 1.1 * 2 * c(1, 2048, 24, 4, 67584, 1)
+    # one TP=2 rank of the reference's shape (12 q / 2 kv heads, bs 1,584): 128 query tiles fill
+    # half the CUs, so 2 splits at every context (0.095 against 0.125 ms at 0 cached tokens, 3.43
+    # against 7.99 ms at 131,072); page tables of bs 1,584 never overflow
+    for ctx in (0, 16384, 65536, 131072):
+        assert ps(1, 2048, 12, 2, ctx + 2048, 1584) == 2
 
 
 def test_prefill_split_validation_messages(lib):
