@@ -79,18 +79,16 @@ template <bool kFast, class P>
 __device__ __forceinline__ void issue_tile(const P& a, const TileSrc& src, const DmaLane& d,
                                            unsigned slot, int lane) {
     if constexpr (kFast) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int8_t* kb = src.base[i >> 2] + (int64_t)(4 * (i & 3)) * a.k_ss;
-            dma16_s(kb, d.kvo, slot + kImgK + i * kBlk);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int8_t* vb = src.base[i >> 2] + (int64_t)(i & 3) * a.k_ss;
-            dma16_s(vb, d.vvo, slot + kImgV + i * kBlk);
-        }
+        static_for<0, 8>([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            dma16_so<kImgK + i * kBlk>(src.base[i >> 2] + (int64_t)(4 * (i & 3)) * a.k_ss, d.kvo, slot);
+        });
+        static_for<0, 8>([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            dma16_so<kImgV + i * kBlk>(src.base[i >> 2] + (int64_t)(i & 3) * a.k_ss, d.vvo, slot);
+        });
         const int64_t delta = src.base[1] - src.base[0];
-        dma16_v<0>(src.base[0] + (delta & -(int64_t)d.tsel) + d.toff, slot + kImgT);
+        dma16_vo<kImgT>(src.base[0] + (delta & -(int64_t)d.tsel) + d.toff, slot);
     } else {
         // chunk-major images: lanes 0-31 copy chunk 2 i of rows 0..31, lanes 32-63 chunk 2 i + 1
         const int8_t* row = src.base[0];  // tile row lane & 31
@@ -330,9 +328,10 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         if (nt > 0) issue_tile<kFast>(a, src0, dl, wslots, l);
         // the K blocks of the second tile follow at once, its other copies after the set-up
         if (nt > 1) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                dma16_s(src1.base[i >> 2] + (int64_t)(4 * (i & 3)) * a.k_ss, dl.kvo, wslots + kSlot + kImgK + i * kBlk);
+            static_for<0, 8>([&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                dma16_so<kSlot + kImgK + i * kBlk>(src1.base[i >> 2] + (int64_t)(4 * (i & 3)) * a.k_ss, dl.kvo, wslots);
+            });
         }
         // (3) wait for (1) only
         if (nt > 1)
@@ -364,12 +363,12 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         }
         __syncthreads();  // the block offsets are visible
         if (nt > 1) {
-            const unsigned slot = wslots + (unsigned)kSlot;
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                dma16_s(src1.base[i >> 2] + (int64_t)(i & 3) * a.k_ss, dl.vvo, slot + kImgV + i * kBlk);
+            static_for<0, 8>([&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                dma16_so<kSlot + kImgV + i * kBlk>(src1.base[i >> 2] + (int64_t)(i & 3) * a.k_ss, dl.vvo, wslots);
+            });
             const int64_t delta = src1.base[1] - src1.base[0];
-            dma16_v<0>(src1.base[0] + (delta & -(int64_t)dl.tsel) + dl.toff, slot + kImgT);
+            dma16_vo<kSlot + kImgT>(src1.base[0] + (delta & -(int64_t)dl.tsel) + dl.toff, wslots);
         }
     } else {
         const int pk_first = max(tb * kTile, lo), pk_last = min(te * kTile, hi) - 1;
@@ -612,9 +611,10 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
             wait_lds();  // every LDS access to the slot being refilled has completed
             nsrc = tile_src<kFast, kLds>(a, pt, gbase, tile_of(n), n, lo, hi, l);
             const unsigned slot = wslots + (unsigned)((n & 1) * kSlot);
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                dma16_s(nsrc.base[i >> 2] + (int64_t)(4 * (i & 3)) * a.k_ss, dl.kvo, slot + kImgK + i * kBlk);
+            static_for<0, 8>([&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                dma16_so<kImgK + i * kBlk>(nsrc.base[i >> 2] + (int64_t)(4 * (i & 3)) * a.k_ss, dl.kvo, slot);
+            });
         };
         // While the stream ramps up (the refills of its first kRampTiles tiles) the first four V
         // blocks go between the scores and the values, the rest after the values.
@@ -622,22 +622,25 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         auto ramp = [&](int n) { return n - 2 < kRampTiles; };  // refill n is issued by iteration n - 2
         auto issue_v0 = [&](int n) __attribute__((always_inline)) {
             const unsigned slot = wslots + (unsigned)((n & 1) * kSlot);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                dma16_s(nsrc.base[i >> 2] + (int64_t)(i & 3) * a.k_ss, dl.vvo, slot + kImgV + i * kBlk);
+            static_for<0, 4>([&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                dma16_so<kImgV + i * kBlk>(nsrc.base[i >> 2] + (int64_t)(i & 3) * a.k_ss, dl.vvo, slot);
+            });
         };
         auto issue_v = [&](int n) __attribute__((always_inline)) {
             const unsigned slot = wslots + (unsigned)((n & 1) * kSlot);
             if (!ramp(n)) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    dma16_s(nsrc.base[i >> 2] + (int64_t)(i & 3) * a.k_ss, dl.vvo, slot + kImgV + i * kBlk);
+                static_for<0, 4>([&](auto ic) {
+                    constexpr int i = decltype(ic)::value;
+                    dma16_so<kImgV + i * kBlk>(nsrc.base[i >> 2] + (int64_t)(i & 3) * a.k_ss, dl.vvo, slot);
+                });
             }
-#pragma unroll
-            for (int i = 4; i < 8; ++i)
-                dma16_s(nsrc.base[i >> 2] + (int64_t)(i & 3) * a.k_ss, dl.vvo, slot + kImgV + i * kBlk);
+            static_for<4, 8>([&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                dma16_so<kImgV + i * kBlk>(nsrc.base[i >> 2] + (int64_t)(i & 3) * a.k_ss, dl.vvo, slot);
+            });
             const int64_t delta = nsrc.base[1] - nsrc.base[0];
-            dma16_v<0>(nsrc.base[0] + (delta & -(int64_t)dl.tsel) + dl.toff, slot + kImgT);
+            dma16_vo<kImgT>(nsrc.base[0] + (delta & -(int64_t)dl.tsel) + dl.toff, slot);
         };
         // The first two tiles (issued during the set-up when kEarly): all loads the compiler can
         // see (Q, block table) have been waited for by now, so no compiler-inserted wait will

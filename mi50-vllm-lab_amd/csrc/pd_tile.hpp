@@ -6,6 +6,8 @@
 // both kernels' GPU tests cover it.
 #pragma once
 
+#include <type_traits>
+
 #include "pd_kernels.hpp"
 
 namespace pd {
@@ -170,6 +172,33 @@ __device__ __forceinline__ void dma16_s(const int8_t* sbase, unsigned voff, unsi
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0)
                  : "memory", "m0");
 }
+// dma16_s into LDS slot + kOff: the destination is formed in m0 by the copy's own s_add (one
+// scalar instruction per copy instead of an add into a register and a move).
+template <int kOff>
+__device__ __forceinline__ void dma16_so(const int8_t* sbase, unsigned voff, unsigned slot) {
+    if constexpr (kOff == 0)
+        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(slot)
+                     : "memory", "m0");
+    else
+        asm volatile("s_add_u32 m0, %2, %3\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(slot),
+                     "i"(kOff)
+                     : "memory", "m0", "scc");
+}
+// The same with a wave-uniform offset held in a scalar register.
+__device__ __forceinline__ void dma16_ss(const int8_t* sbase, unsigned voff, unsigned slot, unsigned off) {
+    asm volatile("s_add_u32 m0, %2, %3\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(slot),
+                 "s"(off)
+                 : "memory", "m0", "scc");
+}
+// Calls f(std::integral_constant<int, I>) for I = kBegin .. kEnd - 1 (copy offsets that the asm
+// takes as immediates must be compile-time constants).
+template <int kBegin, int kEnd, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (kBegin < kEnd) {
+        f(std::integral_constant<int, kBegin>{});
+        static_for<kBegin + 1, kEnd>(f);
+    }
+}
 // The immediate offset applies to the LDS destination too: the copy lands at m0 + kImm +
 // 16 * lane, so m0 is passed already reduced by kImm.
 template <int kImm>
@@ -177,6 +206,12 @@ __device__ __forceinline__ void dma16_v(const int8_t* vaddr, unsigned lds_dst) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off offset:%2" ::"v"(vaddr), "s"(lds_dst - kImm),
                  "i"(kImm)
                  : "memory", "m0");
+}
+// dma16_v<0> into LDS slot + kOff, m0 formed by the copy's own s_add.
+template <int kOff>
+__device__ __forceinline__ void dma16_vo(const int8_t* vaddr, unsigned slot) {
+    asm volatile("s_add_u32 m0, %1, %2\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(vaddr), "s"(slot), "i"(kOff)
+                 : "memory", "m0", "scc");
 }
 // 4-byte copies: LDS[dst + 4 * lane] = *vaddr.
 __device__ __forceinline__ void dma4_v(const int* vaddr, unsigned lds_dst) {
