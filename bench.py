@@ -120,24 +120,37 @@ COUNTERS = ("SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_MFMA", "
 
 
 def summarize_counters(args):
-    """Instruction mix and MFMA utilisation per partial-kernel launch from one rocprofv3 --pmc run
-    of --profile-only with COUNTERS (medians over the dispatches), per wave and per 32-key tile."""
+    """Instruction mix and MFMA utilisation per kernel launch from one rocprofv3 --pmc run with
+    COUNTERS (medians over the dispatches), per wave and per 32-key tile: the decode partial kernel
+    of --profile-only (--counters-kernel partial; a tile is one wave's 32 keys) or the config-5
+    prefill kernel of --profile-prefill (--counters-kernel prefill; a tile is 32 keys that every
+    wave of a workgroup computes for its 48 rows, counted once per wave)."""
+    kind = args.counters_kernel
     per = {c: _pmc_dispatches(args.counters_summary, c) for c in COUNTERS}
     med = {}
     for c, d in per.items():
-        v = sorted(x for name, x in d.values() if "partial" in name)
+        v = sorted(x for name, x in d.values() if kind in name and "combine" not in name)
         if not v:
-            raise SystemExit(f"{c}: no partial-kernel dispatches")
+            raise SystemExit(f"{c}: no {kind}-kernel dispatches")
         med[c] = v[len(v) // 2]
     import workload as wl
 
-    case = decode_case(wl, 2)
-    tiles = 4 * (((case.seq_lens[0].item() - 1) // 32) + 1)  # 32-key tiles over the 4 kv heads
+    if kind == "partial":
+        case = decode_case(wl, 2)
+        tiles = 4 * (((case.seq_lens[0].item() - 1) // 32) + 1)  # 32-key tiles over the 4 kv heads
+        what = {"kernel": "decode partial kernel", "workload": "MTP verify 4 x 24/4 heads, ctx 61440+4, bs 16",
+                "nsplit": args.nsplit}
+    else:
+        # workgroup q of a kv head: tokens [32 q, 32 q + 32) of the chunk, keys [0, ctx + 32 q + 32)
+        tpw = 192 // 6
+        tiles = 4 * sum(-(-min(PREFILL_CTX + PREFILL_CHUNK, PREFILL_CTX + tpw * (q + 1)) // 32)
+                        for q in range(PREFILL_CHUNK // tpw))
+        tiles *= 4  # each of the 4 waves computes every tile of its workgroup
+        what = {"kernel": "chunked prefill kernel", "workload": DESCRIPTIONS[5]}
     waves = med["SQ_WAVES"]
     simd_cycles = med["SQ_BUSY_CU_CYCLES"] / 256 * 1.0  # per CU: 4 SIMDs, each busy that long
     summary = {
-        "kernel": "decode partial kernel", "workload": "MTP verify 4 x 24/4 heads, ctx 61440+4, bs 16",
-        "nsplit": args.nsplit, "counters_median_per_dispatch": {c: round(v) for c, v in med.items()},
+        **what, "counters_median_per_dispatch": {c: round(v) for c, v in med.items()},
         "per_wave": {c: round(med[c] / waves, 1) for c in ("SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_MFMA")},
         "per_tile": {c: round(med[c] / tiles, 1) for c in ("SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_MFMA")},
         "tiles": tiles,
@@ -388,7 +401,10 @@ def main():
     ap.add_argument("--counters-summary", metavar="PMC_DIR",
                     help="no GPU work: turn a rocprofv3 --pmc run of --profile-only with the counters in "
                          "bench.COUNTERS into instruction mix and MFMA utilisation, written to --counters-out")
-    ap.add_argument("--counters-out", default=os.path.join(PROFILES, "pd_partial_mtp61k_counters.json"))
+    ap.add_argument("--counters-out", default=None,
+                    help="default: profiles/pd_partial_mtp61k_counters.json (partial) or "
+                         "profiles/pd_prefill_chunk2048_ctx61440_counters.json (prefill)")
+    ap.add_argument("--counters-kernel", default="partial", choices=("partial", "prefill"))
     ap.add_argument("--prefill-grid", metavar="HQ,HKV,BS",
                     help="the reference's prefill sweep: one 2,048-token chunk over 0/16k/64k/128k cached tokens "
                          "(one JSON line per cell), e.g. 12,2,1584 (one TP=2 rank, as the reference) or 24,4,16")
@@ -401,6 +417,9 @@ def main():
         summarize_traffic(args)
         return
     if args.counters_summary:
+        if args.counters_out is None:
+            args.counters_out = os.path.join(PROFILES, "pd_partial_mtp61k_counters.json" if args.counters_kernel ==
+                                             "partial" else "pd_prefill_chunk2048_ctx61440_counters.json")
         summarize_counters(args)
         return
 
@@ -619,6 +638,11 @@ def bench_prefill(torch, wl, pd, dev, stream, reps=20, exact_too=True):
     line = {"workload": DESCRIPTIONS[5], "ms_per_chunk": round(ms, 4), "TFLOP_s": round(tflops, 1),
             "frac": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4), "flops": flops, "peak": MFMA_FP16_PEAK_TFLOPS,
             "bound": "mfma", "timed": f"{reps // 2} replays of a 2-call graph over 2 cache copies"}
+    ctr = committed_profile("pd_prefill_chunk2048_ctx61440_counters.json")
+    if ctr:
+        line["mfma_busy"] = ctr.get("mfma_busy")
+        line["per_tile"] = ctr.get("per_tile")
+        line["counters_from"] = "profiles/pd_prefill_chunk2048_ctx61440_counters.json"
     if exact_too:
         mse = timed(True)
         tfe = flops / (mse * 1e-3) / 1e12
