@@ -779,10 +779,45 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     }
 }
 
+// Cross-row lane exchanges of gfx950 (v_permlane16/32_swap), as asm with both registers read and
+// written. With a = b = x on entry: permlane16: a = rows (0, 0, 2, 2) of x, b = rows (1, 1, 3, 3);
+// permlane32: a = (low, low) halves, b = (high, high). So a op b is x op x^16 (resp. x^32) in
+// every lane, with no LDS crossbar round trip. The swap must not read a register a VALU
+// instruction has just written, and the compiler inserts no wait states around asm: the
+// s_nop before (and after, for the results) supply them.
+__device__ __forceinline__ void permlane16_swap(float& a, float& b) {
+    asm volatile("s_nop 4\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 4" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane32_swap(float& a, float& b) {
+    asm volatile("s_nop 4\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 4" : "+v"(a), "+v"(b));
+}
+template <int kCtrl>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float xor16_sum(float x) {
+    float a = x, b = x;
+    permlane16_swap(a, b);
+    return a + b;
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+    float a = x, b = x;
+    permlane32_swap(a, b);
+    return a + b;
+}
+// Max over the 64 lanes, in every lane: DPP within 16-lane rows (quad swaps of 1 and 2 lanes, the
+// half-row and row mirrors), then the two cross-row swaps.
 __device__ __forceinline__ float wave_max64(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+    v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+    v = fmaxf(v, dpp_mov<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_mov<0x140>(v));  // row_mirror
+    float a = v, b = v;
+    permlane16_swap(a, b);
+    v = fmaxf(a, b);
+    a = v, b = v;
+    permlane32_swap(a, b);
+    return fmaxf(a, b);
 }
 
 // Log-sum-exp merge of the split partials (pth_dec.cu:245-283 semantics): M = max_p m_p,
@@ -802,8 +837,16 @@ __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = tid % kCols, sg = tid / kCols;
 
-    // The partial loads go out first: they are in bounds for every (token, head) of the grid, and
-    // the sequence lookup below (two dependent small loads) then overlaps their latency.
+    // Sequence of this token = number of sequences whose query rows end at or before it. The first
+    // 64 sequences' ends are requested before the partial loads, so that waiting for them does not
+    // wait for the partials; the entry of the token's sequence then comes by scalar loads while
+    // the partial loads are in flight. The lookup only gates the final store (the merge of a
+    // padding token reads allocated but unwritten partials and is discarded).
+    // (Every load below is unconditional, from a clamped index with the value selected afterwards,
+    // so that the compiler can count them and wait for exactly the one it needs.)
+    const int q_end_ld = a.qsl[min(lane + 1, a.num_seqs)];
+    asm volatile("" ::: "memory");  // issued before the partial loads
+    // The partial loads are in bounds for every (token, head) of the grid.
     const int64_t base = ((int64_t)tok * Hq + head) * a.nseg;
     const float* pm = a.part_m + base;
     const float* pl = a.part_l + base;
@@ -815,22 +858,23 @@ __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) 
     for (int i = 0; i < kCombPer; ++i) {
         const int sgi = sg + kGroups * i;
         const bool ok = sgi < a.nsplit;
-        mv[i] = ok ? pm[sgi] : kNegInf;
-        lv[i] = ok ? pl[sgi] : 0.f;
-        ov[i] = ok ? po[(int64_t)sgi * (kDim / 4)] : (float4_t)0.f;
+        const int si = min(sgi, a.nsplit - 1);
+        const float m = pm[si], lw = pl[si];
+        const float4_t o = po[(int64_t)si * (kDim / 4)];
+        mv[i] = ok ? m : kNegInf;
+        lv[i] = ok ? lw : 0.f;
+        ov[i] = ok ? o : (float4_t)0.f;
     }
 
-    // sequence of this token = number of sequences whose query rows end at or before it; the
-    // lookup only gates the final store, so its loads overlap the merge (the merge of a padding
-    // token reads allocated but unwritten partials and is discarded)
-    int b = 0;
-    for (int i0 = 0; i0 < a.num_seqs; i0 += 64) {
+    const int q_end0 = lane + 1 <= a.num_seqs ? q_end_ld : 0x7fffffff;
+    int b = __popcll(__ballot(q_end0 <= tok));
+    for (int i0 = 64; i0 < a.num_seqs; i0 += 64) {
         const int i = i0 + lane + 1;
         const bool ended = i <= a.num_seqs && a.qsl[i] <= tok;
         b += __popcll(__ballot(ended));
     }
-    const int bq = min(b, a.num_seqs - 1);
-    const int q_b = a.qsl[bq], len_b = a.seq_lens[bq];
+    const int bq = __builtin_amdgcn_readfirstlane(min(b, a.num_seqs - 1));
+    const int q_b = ((const_int_ptr)(uintptr_t)a.qsl)[bq], len_b = ((const_int_ptr)(uintptr_t)a.seq_lens)[bq];
     const bool live = b < a.num_seqs && tok >= q_b && len_b > 0 && tok - q_b < a.qmax;
     float mx = kNegInf;
 #pragma unroll
@@ -859,15 +903,20 @@ __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) 
             }
         }
     }
-    // reduce over the 16 segment slots: xor 16 / 32 inside the wave, then across the 4 waves
-#pragma unroll
-    for (int o = kCols; o <= 32; o <<= 1) {
-        lsum += __shfl_xor(lsum, o, 64);
-        acc.x += __shfl_xor(acc.x, o, 64);
-        acc.y += __shfl_xor(acc.y, o, 64);
-        acc.z += __shfl_xor(acc.z, o, 64);
-        acc.w += __shfl_xor(acc.w, o, 64);
+    // reduce over the segment slots: lanes 16 and 32 apart inside the wave (32 only for half
+    // rows), then across the 4 waves
+    if constexpr (kCols == 16) {
+        lsum = xor16_sum(lsum);
+        acc.x = xor16_sum(acc.x);
+        acc.y = xor16_sum(acc.y);
+        acc.z = xor16_sum(acc.z);
+        acc.w = xor16_sum(acc.w);
     }
+    lsum = xor32_sum(lsum);
+    acc.x = xor32_sum(acc.x);
+    acc.y = xor32_sum(acc.y);
+    acc.z = xor32_sum(acc.z);
+    acc.w = xor32_sum(acc.w);
     if (lane < kCols) s_acc[wave][lane] = acc;
     if (lane == 0) s_l[wave] = lsum;
     __syncthreads();
