@@ -820,22 +820,41 @@ __device__ __forceinline__ float wave_max64(float v) {
     return fmaxf(a, b);
 }
 
+// Sum over the 64 lanes, in every lane (the same DPP and swap steps as wave_max64).
+__device__ __forceinline__ float wave_sum64(float v) {
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    v += dpp_mov<0x140>(v);
+    return xor32_sum(xor16_sum(v));
+}
+
+// Sum of a float4 over the lanes of the wave that share lane % kCW (kCW = 4 or 8): rotations by 4
+// and 8 lanes inside each 16-lane row (DPP row_ror), then the two cross-row swaps.
+template <int kCW>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (kCW == 4) v += dpp_mov<0x124>(v);  // row_ror:4
+    v += dpp_mov<0x128>(v);                          // row_ror:8
+    return xor32_sum(xor16_sum(v));
+}
+
 // Log-sum-exp merge of the split partials (pth_dec.cu:245-283 semantics): M = max_p m_p,
 // L = sum_p 2^(m_p - M) l_p, out = sum_p 2^(m_p - M) O_p / L, and 0 when L == 0. Grid
-// (num_tokens, heads_q, 64 / kCols): each workgroup merges 4 kCols dims of one (token, head)
-// row. Thread (sg = tid / kCols, c = tid % kCols) owns float4 column c of segments sg, sg +
-// 256 / kCols, ...; all partial loads of the first 64 segments are issued before the one
-// barrier that publishes M, so the merge costs one memory round trip.
+// (num_tokens, heads_q, 64 / kCols): a workgroup merges 4 kCols dims of one (token, head) row, and
+// each of its 4 waves a quarter of them (kCW float4 columns) over every split, so the waves never
+// exchange data: no LDS and no barrier. Lane (sg, c) of a wave owns column c of splits sg, sg +
+// 64 / kCW, ...; M and L come from a second layout in which lane s holds split s's m and l, by
+// wave reductions. Every partial load is issued before anything waits, so the merge costs one
+// memory round trip.
 template <int kCols>  // float4 columns per workgroup: 16 (a 64-dim quarter) or 32 (a half row)
 __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) {
-    constexpr int kGroups = 256 / kCols;  // segment groups
-    constexpr int kCombPer = 64 / kGroups;  // segments per thread in the first pass
-    __shared__ float s_red[4];
-    __shared__ float s_l[4];
-    __shared__ float4_t s_acc[4][kCols];
-    const int tok = blockIdx.x, head = blockIdx.y, quarter = blockIdx.z, Hq = gridDim.y;
+    constexpr int kCW = kCols / 4;  // float4 columns per wave
+    constexpr int kSG = 64 / kCW;   // lanes sharing a column (segment groups)
+    constexpr int kPer = 64 / kSG;  // segments per lane among the first 64
+    const int tok = blockIdx.x, head = blockIdx.y, part = blockIdx.z, Hq = gridDim.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int c = tid % kCols, sg = tid / kCols;
+    const int c = lane % kCW, sg = lane / kCW;
+    const int col = wave * kCW + c;  // float4 column within the workgroup's dims
 
     // Sequence of this token = number of sequences whose query rows end at or before it. The first
     // 64 sequences' ends are requested before the partial loads, so that waiting for them does not
@@ -850,20 +869,18 @@ __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) 
     const int64_t base = ((int64_t)tok * Hq + head) * a.nseg;
     const float* pm = a.part_m + base;
     const float* pl = a.part_l + base;
-    const float4_t* po = reinterpret_cast<const float4_t*>(a.part_o + base * kDim + quarter * 4 * kCols) + c;
-
-    float mv[kCombPer], lv[kCombPer];
-    float4_t ov[kCombPer];
+    const float4_t* po = reinterpret_cast<const float4_t*>(a.part_o + base * kDim + part * 4 * kCols) + col;
+    const int ns1 = a.nsplit - 1;
+    const float m_ld = pm[min(lane, ns1)], l_ld = pl[min(lane, ns1)];  // lane s: split s
+    float mv[kPer];
+    float4_t ov[kPer];
 #pragma unroll
-    for (int i = 0; i < kCombPer; ++i) {
-        const int sgi = sg + kGroups * i;
-        const bool ok = sgi < a.nsplit;
-        const int si = min(sgi, a.nsplit - 1);
-        const float m = pm[si], lw = pl[si];
+    for (int i = 0; i < kPer; ++i) {
+        const int si = min(sg + kSG * i, ns1);
+        const float m = pm[si];
         const float4_t o = po[(int64_t)si * (kDim / 4)];
-        mv[i] = ok ? m : kNegInf;
-        lv[i] = ok ? lw : 0.f;
-        ov[i] = ok ? o : (float4_t)0.f;
+        mv[i] = sg + kSG * i <= ns1 ? m : kNegInf;
+        ov[i] = o;
     }
 
     const int q_end0 = lane + 1 <= a.num_seqs ? q_end_ld : 0x7fffffff;
@@ -876,58 +893,41 @@ __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) 
     const int bq = __builtin_amdgcn_readfirstlane(min(b, a.num_seqs - 1));
     const int q_b = ((const_int_ptr)(uintptr_t)a.qsl)[bq], len_b = ((const_int_ptr)(uintptr_t)a.seq_lens)[bq];
     const bool live = b < a.num_seqs && tok >= q_b && len_b > 0 && tok - q_b < a.qmax;
-    float mx = kNegInf;
-#pragma unroll
-    for (int i = 0; i < kCombPer; ++i) mx = fmaxf(mx, mv[i]);
-    for (int p = tid + kGroups * kCombPer; p < a.nsplit; p += 256) mx = fmaxf(mx, pm[p]);
-    mx = wave_max64(mx);
-    if (lane == 0) s_red[wave] = mx;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
 
-    float lsum = 0.f;
+    // M and L over the splits, in the split-per-lane layout (splits 64.. one per lane more)
+    const float m_s = lane <= ns1 ? m_ld : kNegInf;
+    float mx = m_s;
+    for (int p = 64 + lane; p <= ns1; p += 64) mx = fmaxf(mx, pm[p]);
+    const float M = wave_max64(mx);
+    float lw = 0.f;
     float4_t acc = (float4_t)0.f;
     if (M != kNegInf) {
+        lw = m_s != kNegInf ? exp2f(m_s - M) * l_ld : 0.f;
+        for (int p = 64 + lane; p <= ns1; p += 64) {
+            const float mp = pm[p];
+            if (mp != kNegInf) lw += exp2f(mp - M) * pl[p];
+        }
 #pragma unroll
-        for (int i = 0; i < kCombPer; ++i) {
+        for (int i = 0; i < kPer; ++i) {
             const float w = mv[i] != kNegInf ? exp2f(mv[i] - M) : 0.f;
-            lsum += w * lv[i];
             acc += w != 0.f ? w * ov[i] : (float4_t)0.f;  // empty splits leave part_o unwritten
         }
-        for (int p = sg + kGroups * kCombPer; p < a.nsplit; p += kGroups) {
+        for (int p = sg + 64; p <= ns1; p += kSG) {
             const float mp = pm[p];
-            const float w = mp != kNegInf ? exp2f(mp - M) : 0.f;
-            if (w != 0.f) {
-                lsum += w * pl[p];
-                acc += w * po[(int64_t)p * (kDim / 4)];
-            }
+            if (mp != kNegInf) acc += exp2f(mp - M) * po[(int64_t)p * (kDim / 4)];
         }
     }
-    // reduce over the segment slots: lanes 16 and 32 apart inside the wave (32 only for half
-    // rows), then across the 4 waves
-    if constexpr (kCols == 16) {
-        lsum = xor16_sum(lsum);
-        acc.x = xor16_sum(acc.x);
-        acc.y = xor16_sum(acc.y);
-        acc.z = xor16_sum(acc.z);
-        acc.w = xor16_sum(acc.w);
-    }
-    lsum = xor32_sum(lsum);
-    acc.x = xor32_sum(acc.x);
-    acc.y = xor32_sum(acc.y);
-    acc.z = xor32_sum(acc.z);
-    acc.w = xor32_sum(acc.w);
-    if (lane < kCols) s_acc[wave][lane] = acc;
-    if (lane == 0) s_l[wave] = lsum;
-    __syncthreads();
-    if (live && tid < kCols) {
-        const float4_t r = s_acc[0][tid] + s_acc[1][tid] + s_acc[2][tid] + s_acc[3][tid];
-        const float L = s_l[0] + s_l[1] + s_l[2] + s_l[3];
+    const float L = wave_sum64(lw);
+    acc.x = group_sum<kCW>(acc.x);
+    acc.y = group_sum<kCW>(acc.y);
+    acc.z = group_sum<kCW>(acc.z);
+    acc.w = group_sum<kCW>(acc.w);
+    if (live && sg == 0) {
         const float inv = L > 0.f ? 1.f / L : 0.f;
         typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-        const half4_t h = {(_Float16)(r.x * inv), (_Float16)(r.y * inv), (_Float16)(r.z * inv),
-                           (_Float16)(r.w * inv)};
-        _Float16* o = a.out + (int64_t)tok * a.o_st + (int64_t)head * a.o_sh + quarter * 4 * kCols + 4 * tid;
+        const half4_t h = {(_Float16)(acc.x * inv), (_Float16)(acc.y * inv), (_Float16)(acc.z * inv),
+                           (_Float16)(acc.w * inv)};
+        _Float16* o = a.out + (int64_t)tok * a.o_st + (int64_t)head * a.o_sh + part * 4 * kCols + 4 * col;
         __builtin_memcpy(o, &h, 8);
     }
 }
