@@ -194,7 +194,7 @@ def test_outlier_rows_within_fp16_weight_rounding():
 
 
 def test_exact_outlier_rows_within_decode_tolerance():
-    """pth_fa_forward_exact on the outlier case above: K is widened without bias and P' is
+    """pth_fa_forward_exact on the outlier case above: K and V are widened without bias and P' is
     carried as fp16 hi + lo, so the P' rounding (2^-12 relative per weight, times |V| up to 50
     v_scale) drops to ~2^-23 and the plain bar holds: max-abs <= 2e-3, mean-abs <= 2e-4. A second
     case puts 2% of the rows at 100x, with a 640-key context and the chunk inside the cache."""
