@@ -702,10 +702,24 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     {
         // Each wave stores its accumulators as they are (a 1 KiB block per accumulator and row
         // block, straight from the AGPRs: no vector ALU work) into its own slots as soon as its
-        // tiles are done, with its per-row max and sum; then thread (row, 32
-        // dims) derives the wave factors of its row, sums the four waves' blocks with them and
-        // writes the partial row. Row blocks go through the slots two at a time (kRawRounds
-        // rounds).
+        // tiles are done, with its per-row max and sum. Row blocks go through the slots two at a
+        // time (kRawRounds rounds). Dims of an accumulator block: block m < 16 holds dims
+        // 16 m - 4 + 4 lg .. + 3 in lane group lg (row li), block 16 holds 244..255 in lane
+        // groups 0-2. Row factors: M = max_w m_w, e_w = 2^(m_w - M), O = sum_w e_w O_w / 16,
+        // L = sum_w e_w l_w.
+        //
+        // Two or three row blocks: thread (row, 32 dims) derives the factors of its row, sums the
+        // four waves' blocks with them and writes its part of the row (a block holds the float4 of
+        // (lg, row rr) at 16 lg + rr).
+        //
+        // One row block (at most 16 rows, single-token decodes): each wave takes whole rows, so
+        // the lanes of rows that do not exist issue nothing. For one row the 64 lanes read dims
+        // 4 L .. 4 L + 3 (block (L + 1) / 4, group (L + 1) % 4) and store the row's 1 KiB with one
+        // instruction. A block then holds the float4 of (lg, rr) at 16 lg + ((rr + lg + 4 (m & 3))
+        // & 15), so that the row reads (position (rr + L + 1) & 15) and the stores (16 rows of
+        // one lane group) both spread over all banks. (With two row blocks this layout measured
+        // 0.26 us slower per launch at 24 rows.)
+        constexpr bool kRowStores = NRB == 1;
         constexpr int kRawRounds = (NRB + 1) / 2;
         float* wm = reinterpret_cast<float*>(lds + kLdsStats);  // [wave][NRB][16] running max
         float* wl = wm + kWaves * NRB * 16;                     // [wave][NRB][16] row sum of p
@@ -717,64 +731,100 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
                 wl[(w * NRB + rb) * 16 + li] = l_row;
             }
         }
-        const unsigned raw = lds_base + (unsigned)(w * kWaveLds + 16 * l);  // this wave's slots
+        unsigned raw[4];  // this wave's slots, by block index m & 3
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            raw[k] = lds_base + (unsigned)(w * kWaveLds + 16 * (kRowStores ? 16 * lg + ((li + lg + 4 * k) & 15) : l));
         auto store_round = [&](int rd) __attribute__((always_inline)) {
 #pragma unroll
             for (int rb = 2 * rd; rb < 2 * rd + 2 && rb < NRB; ++rb)
 #pragma unroll
                 for (int m = 0; m < 17; ++m)
-                    asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(raw), "a"(oacc[rb][m]),
+                    asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(raw[m & 3]), "a"(oacc[rb][m]),
                                  "i"(((rb - 2 * rd) * 17 + m) * 1024)
                                  : "memory");
         };
         store_round(0);
         wait_lds();
         __syncthreads();  // every wave's stats and first accumulator blocks are in LDS
+        auto factors = [&](int row, float* f) __attribute__((always_inline)) {
+            float M = kNegInf;
 #pragma unroll
-        for (int rd = 0; rd < kRawRounds; ++rd) {
-            if (rd > 0) {
-                store_round(rd);
-                wait_lds();
-                __syncthreads();
+            for (int v = 0; v < kWaves; ++v) M = fmaxf(M, wm[v * NRB * 16 + row]);
+            float Lr = 0.f;
+#pragma unroll
+            for (int v = 0; v < kWaves; ++v) {
+                const float mw = wm[v * NRB * 16 + row];
+                const float e = mw == kNegInf ? 0.f : exp2f(mw - M);
+                f[v] = e * (1.0f / kPScale);
+                Lr += e * wl[v * NRB * 16 + row];
             }
-            // thread: row 32 rd + (lane & 31), wave w's two 32-dim parts. Row factors: M =
-            // max_w m_w, e_w = 2^(m_w - M), O = sum_w e_w O_w / 16, L = sum_w e_w l_w. Dims d of
-            // an accumulator block: block m < 16 holds 16 m - 4 + 4 lg
-            // .. + 3 in lane group lg, block 16 holds 252..255 in lane group 2
-            const int row = 32 * rd + (l & 31), part = 2 * w + (l >> 5);
-            if (row < R) {
-                float M = kNegInf;
-#pragma unroll
-                for (int v = 0; v < kWaves; ++v) M = fmaxf(M, wm[v * NRB * 16 + row]);
-                float f[kWaves], Lr = 0.f;
-#pragma unroll
-                for (int v = 0; v < kWaves; ++v) {
-                    const float mw = wm[v * NRB * 16 + row];
-                    const float e = mw == kNegInf ? 0.f : exp2f(mw - M);
-                    f[v] = e * (1.0f / kPScale);
-                    Lr += e * wl[v * NRB * 16 + row];
-                }
-                const int64_t pr = prow(row);
-                if (part == 0) {
-                    a.part_m[pr] = M;
-                    a.part_l[pr] = Lr;
-                }
-                const int rbl = (row >> 4) - 2 * rd;  // row block within the round
-                float* dst = a.part_o + pr * kDim;
-                const float4_t* rawp = reinterpret_cast<const float4_t*>(lds);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int d = 32 * part + 4 * j;
-                    const int m = d < 252 ? (d + 4) >> 4 : 16;
-                    const int glg = d < 252 ? ((d + 4) >> 2) & 3 : 2;
-                    const int blk = (rbl * 17 + m) * 64 + 16 * glg + (row & 15);
-                    float4_t acc = rawp[blk] * f[0];
-#pragma unroll
-                    for (int v = 1; v < kWaves; ++v) acc += rawp[v * (kWaveLds / 16) + blk] * f[v];
-                    *reinterpret_cast<float4_t*>(dst + d) = acc;
-                }
+            return float2_t{M, Lr};
+        };
+        if constexpr (kRowStores) {
+            // wave w takes rows w + 4 j; lane j computes the factors of row j of its wave, which
+            // are then read from it as scalars
+            const int rown = w + 4 * (l & 3);
+            float f[kWaves];
+            const float2_t ml = factors(rown, f);
+            if (l < 4 && rown < R) {
+                const int64_t pr = prow(rown);
+                a.part_m[pr] = ml.x;
+                a.part_l[pr] = ml.y;
             }
-            if (rd + 1 < kRawRounds) __syncthreads();  // the blocks are rewritten for the next round
+            const int m_l = l < 63 ? (l + 1) >> 2 : 16;
+            const int g_l = l < 63 ? (l + 1) & 3 : 2;
+            const lds_u8* rd_base = L + (m_l * 1024 + 256 * g_l);
+            const int c_l = g_l + 4 * (m_l & 3);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int row = w + 4 * j;  // uniform
+                if (row >= R) break;
+                const lds_u8* p = rd_base + 16 * ((row + c_l) & 15);
+                float fs[kWaves];
+#pragma unroll
+                for (int v = 0; v < kWaves; ++v)
+                    fs[v] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f[v]), j));
+                float4_t acc = *(const lds_float4*)p * fs[0];
+#pragma unroll
+                for (int v = 1; v < kWaves; ++v) acc += *(const lds_float4*)(p + v * kWaveLds) * fs[v];
+                *reinterpret_cast<float4_t*>(a.part_o + prow(row) * kDim + 4 * l) = acc;
+            }
+        } else {
+#pragma unroll
+            for (int rd = 0; rd < kRawRounds; ++rd) {
+                if (rd > 0) {
+                    store_round(rd);
+                    wait_lds();
+                    __syncthreads();
+                }
+                // thread: row 32 rd + (lane & 31), wave w's two 32-dim parts
+                const int row = 32 * rd + (l & 31), part = 2 * w + (l >> 5);
+                if (row < R) {
+                    float f[kWaves];
+                    const float2_t ml = factors(row, f);
+                    const int64_t pr = prow(row);
+                    if (part == 0) {
+                        a.part_m[pr] = ml.x;
+                        a.part_l[pr] = ml.y;
+                    }
+                    const int rbl = (row >> 4) - 2 * rd;  // row block within the round
+                    float* dst = a.part_o + pr * kDim;
+                    const float4_t* rawp = reinterpret_cast<const float4_t*>(lds);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int d = 32 * part + 4 * j;
+                        const int m = d < 252 ? (d + 4) >> 4 : 16;
+                        const int glg = d < 252 ? ((d + 4) >> 2) & 3 : 2;
+                        const int blk = (rbl * 17 + m) * 64 + 16 * glg + (row & 15);
+                        float4_t acc = rawp[blk] * f[0];
+#pragma unroll
+                        for (int v = 1; v < kWaves; ++v) acc += rawp[v * (kWaveLds / 16) + blk] * f[v];
+                        *reinterpret_cast<float4_t*>(dst + d) = acc;
+                    }
+                }
+                if (rd + 1 < kRawRounds) __syncthreads();  // the blocks are rewritten for the next round
+            }
         }
     }
 }

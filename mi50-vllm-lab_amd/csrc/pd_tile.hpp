@@ -14,12 +14,14 @@ namespace pd {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
 typedef int int2_t __attribute__((ext_vector_type(2)));
 typedef unsigned uint4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
 typedef __attribute__((address_space(3))) int2_t lds_int2;
 typedef __attribute__((address_space(3))) uint4_t lds_uint4;
 typedef __attribute__((address_space(3))) float lds_float;
+typedef __attribute__((address_space(3))) float4_t lds_float4;
 typedef __attribute__((address_space(3))) int lds_int;
 typedef __attribute__((address_space(3))) uint64_t lds_u64;
 typedef unsigned long long ull2_t __attribute__((ext_vector_type(2)));
