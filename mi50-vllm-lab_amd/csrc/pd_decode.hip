@@ -555,9 +555,10 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
             for (int e = 0; e < 8; ++e) {
                 const float p = __builtin_amdgcn_exp2f(sv[rb][e]);  // masked: 2^-inf = 0
                 psum += p;
-                const _Float16 h = (_Float16)(p * vsc[e]);
+                _Float16 h, lo;
+                split_fp16(p, vsc[e], h, lo);
                 phi[rb][e] = h;
-                plo[rb][e] = (_Float16)__builtin_fmaf(p, vsc[e], -(float)h);
+                plo[rb][e] = lo;
             }
             l_run[rb] += psum;
         }

@@ -424,9 +424,14 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
             for (int e = 0; e < 8; ++e) {
                 const float p = __builtin_amdgcn_exp2f(sv[rb][e]);
                 psum += p;
-                const _Float16 h = (_Float16)(p * vs[e]);
-                pop[rb][e] = h;
-                if constexpr (kExact) plo[rb][e] = (_Float16)__builtin_fmaf(p, vs[e], -(float)h);
+                if constexpr (kExact) {
+                    _Float16 h, lo;
+                    split_fp16(p, vs[e], h, lo);
+                    pop[rb][e] = h;
+                    plo[rb][e] = lo;
+                } else {
+                    pop[rb][e] = (_Float16)(p * vs[e]);
+                }
             }
             l_run[rb] += psum;
         }

@@ -94,6 +94,19 @@ __device__ __forceinline__ half8_t widen_i8x8_exact(unsigned w0, unsigned w1) {
     return __builtin_bit_cast(half8_t, h);
 }
 
+// x = p * s as two fp16 parts, hi + lo with ~22 significant bits: hi is the fp32 product rounded
+// to fp16, lo = fp16(p * s - hi) with the product exact (fma). hi must be the same value in both
+// places. The fp32 product is therefore pinned in a register: left to itself the compiler folds
+// the product into the conversion for one use (v_fma_mix, a single rounding of p * s) and keeps a
+// multiply and a convert (two roundings) for the other, and when the fp32 product is an fp16 tie
+// the two roundings differ by an fp16 ulp, so hi + lo misses x by up to 2^-10 relative.
+__device__ __forceinline__ void split_fp16(float p, float s, _Float16& hi, _Float16& lo) {
+    float prod = p * s;
+    asm("" : "+v"(prod));
+    hi = (_Float16)prod;
+    lo = (_Float16)__builtin_fmaf(p, s, -(float)hi);
+}
+
 __device__ __forceinline__ float xor_max(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, 64)); }
 __device__ __forceinline__ float xor_sum(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
 

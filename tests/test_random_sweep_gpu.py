@@ -108,7 +108,11 @@ def draw_decode(i):
     )
 
 
-@pytest.mark.parametrize("i", range(N_DECODE))
+# Seed 4939 holds a P' value whose fp32 product p * v_scale * 16 is an fp16 tie (2.7568359375),
+# on a row whose output is dominated by an outlier V row (v_scale 1.22). When the kernel's hi
+# and the hi subtracted to form lo were rounded differently (two roundings against one), that
+# key's weight was off by 2^-10 relative and the output by 3.2e-3; kept as a regression case.
+@pytest.mark.parametrize("i", list(range(N_DECODE)) + [4939])
 def test_decode_random(i):
     p = draw_decode(i)
     say(f"decode sweep {i}: {p}")
