@@ -26,6 +26,8 @@ Tolerance, on the rows that the reference writes:
   within 2e-3 there. A correctly rounded answer fp16(ref) scores the same as the kernel on such
   a case: max-abs 6.24e-2 against 6.26e-2, mean-abs 1.971e-4 against 1.975e-4.
 
+Eight more decode cases redraw the contexts at 1,000-150,000 keys (draw_decode_long).
+
 Each case prints its parameters before it runs.
 """
 import math
@@ -114,7 +116,33 @@ def draw_decode(i):
 # key's weight was off by 2^-10 relative and the output by 3.2e-3; kept as a regression case.
 @pytest.mark.parametrize("i", list(range(N_DECODE)) + [4939])
 def test_decode_random(i):
+    run_decode_case(i, draw_decode(i))
+
+
+N_DECODE_LONG = 8
+
+
+def draw_decode_long(i):
+    """The decode draw with 1-3 sequences of 1,000-150,000 keys (log-uniform), so that the splits
+    interleave their tiles and page tables outgrow the kernel's LDS copy; block size 1 becomes 16
+    (a 150k-page table of one-key pages takes too long to build here)."""
     p = draw_decode(i)
+    rng = np.random.default_rng(123456 + i)
+    n = min(len(p["ctxs"]), 3)
+    p["ctxs"] = [int(math.exp(rng.uniform(math.log(1000), math.log(150000)))) for _ in range(n)]
+    p["qlens"] = p["qlens"][:n]
+    p["qlens"][0] = p["qmax"]
+    if p["bs"] == 1:
+        p["bs"] = 16
+    return p
+
+
+@pytest.mark.parametrize("i", range(N_DECODE_LONG))
+def test_decode_random_long(i):
+    run_decode_case(i, draw_decode_long(i))
+
+
+def run_decode_case(i, p):
     say(f"decode sweep {i}: {p}")
     c = kvc.make_case(p["ctxs"], p["qlens"], num_q_heads=p["hq"], num_kv_heads=p["hkv"], block_size=p["bs"],
                       layout=p["layout"], seed=p["seed"], kv_mode=p["kv_mode"], outlier_frac=p["outlier"],
