@@ -552,13 +552,17 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         for (int rb = 0; rb < NRB; ++rb) {
             float psum = 0.f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float p = __builtin_amdgcn_exp2f(sv[rb][e]);  // masked: 2^-inf = 0
-                psum += p;
-                _Float16 h, lo;
-                split_fp16(p, vsc[e], h, lo);
-                phi[rb][e] = h;
-                plo[rb][e] = lo;
+            for (int e = 0; e < 8; e += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(sv[rb][e]);  // masked: 2^-inf = 0
+                const float p1 = __builtin_amdgcn_exp2f(sv[rb][e + 1]);
+                psum += p0;
+                psum += p1;
+                half2_t h, lo;
+                split_fp16x2(p0, vsc[e], p1, vsc[e + 1], h, lo);
+                phi[rb][e] = h.x;
+                phi[rb][e + 1] = h.y;
+                plo[rb][e] = lo.x;
+                plo[rb][e + 1] = lo.y;
             }
             l_run[rb] += psum;
         }

@@ -13,6 +13,7 @@
 namespace pd {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
 typedef int int2_t __attribute__((ext_vector_type(2)));
@@ -105,6 +106,15 @@ __device__ __forceinline__ void split_fp16(float p, float s, _Float16& hi, _Floa
     asm("" : "+v"(prod));
     hi = (_Float16)prod;
     lo = (_Float16)__builtin_fmaf(p, s, -(float)hi);
+}
+
+// split_fp16 for two values at once: both hi are converted by one packed conversion, and each lo
+// reads its hi from the packed pair.
+__device__ __forceinline__ void split_fp16x2(float p0, float s0, float p1, float s1, half2_t& hi, half2_t& lo) {
+    float a = p0 * s0, b = p1 * s1;
+    asm("" : "+v"(a), "+v"(b));
+    hi = __builtin_convertvector((float2_t){a, b}, half2_t);
+    lo = (half2_t){(_Float16)__builtin_fmaf(p0, s0, -(float)hi.x), (_Float16)__builtin_fmaf(p1, s1, -(float)hi.y)};
 }
 
 __device__ __forceinline__ float xor_max(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, 64)); }
