@@ -421,16 +421,21 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
         for (int rb = 0; rb < kFaRB; ++rb) {
             float psum = 0.f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float p = __builtin_amdgcn_exp2f(sv[rb][e]);
-                psum += p;
+            for (int e = 0; e < 8; e += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(sv[rb][e]);
+                const float p1 = __builtin_amdgcn_exp2f(sv[rb][e + 1]);
+                psum += p0;
+                psum += p1;
                 if constexpr (kExact) {
-                    _Float16 h, lo;
-                    split_fp16(p, vs[e], h, lo);
-                    pop[rb][e] = h;
-                    plo[rb][e] = lo;
+                    half2_t ph, pl;
+                    split_fp16x2(p0, vs[e], p1, vs[e + 1], ph, pl);
+                    pop[rb][e] = ph.x;
+                    pop[rb][e + 1] = ph.y;
+                    plo[rb][e] = pl.x;
+                    plo[rb][e + 1] = pl.y;
                 } else {
-                    pop[rb][e] = (_Float16)(p * vs[e]);
+                    pop[rb][e] = (_Float16)(p0 * vs[e]);
+                    pop[rb][e + 1] = (_Float16)(p1 * vs[e + 1]);
                 }
             }
             l_run[rb] += psum;
