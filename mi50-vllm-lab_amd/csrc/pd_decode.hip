@@ -901,11 +901,14 @@ __device__ __forceinline__ float group_sum(float v) {
 // 64 / kCW, ...; M and L come from a second layout in which lane s holds split s's m and l, by
 // wave reductions. Every partial load is issued before anything waits, so the merge costs one
 // memory round trip.
-template <int kCols>  // float4 columns per workgroup: 16 (a 64-dim quarter) or 32 (a half row)
+// kCols: float4 columns per workgroup, 16 (a 64-dim quarter) or 32 (a half row); kPer: splits
+// per lane loaded up front (the first kPer * 64 / (kCols / 4) splits), the smallest power of two
+// that covers nsplit up to 64, so that few splits do not cost loads of clamped duplicates.
+template <int kCols, int kPer>
 __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) {
     constexpr int kCW = kCols / 4;  // float4 columns per wave
     constexpr int kSG = 64 / kCW;   // lanes sharing a column (segment groups)
-    constexpr int kPer = 64 / kSG;  // segments per lane among the first 64
+    static_assert(kPer * kSG <= 64, "the up-front loads cover at most the first 64 splits");
     const int tok = blockIdx.x, head = blockIdx.y, part = blockIdx.z, Hq = gridDim.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = lane % kCW, sg = lane / kCW;
@@ -967,7 +970,7 @@ __global__ void __launch_bounds__(256) pd_combine_kernel(const CombineParams a) 
             const float w = mv[i] != kNegInf ? exp2f(mv[i] - M) : 0.f;
             acc += w != 0.f ? w * ov[i] : (float4_t)0.f;  // empty splits leave part_o unwritten
         }
-        for (int p = sg + 64; p <= ns1; p += kSG) {
+        for (int p = sg + kSG * kPer; p <= ns1; p += kSG) {
             const float mp = pm[p];
             if (mp != kNegInf) acc += exp2f(mp - M) * po[(int64_t)p * (kDim / 4)];
         }
@@ -1047,6 +1050,20 @@ hipError_t launch_partial(const LaunchArgs& x, hipStream_t stream) {
     return launch_partial_nrb<3>(p, grid, stream, fast);
 }
 
+template <int kCols>
+static void launch_combine_cols(const CombineParams& c, dim3 grid, hipStream_t stream) {
+    constexpr int kSG = 64 / (kCols / 4);
+    const int need = (min(c.nsplit, 64) + kSG - 1) / kSG;  // splits per lane to cover
+    if (need <= 1)
+        hipLaunchKernelGGL((pd_combine_kernel<kCols, 1>), grid, dim3(256), 0, stream, c);
+    else if (need <= 2)
+        hipLaunchKernelGGL((pd_combine_kernel<kCols, 2>), grid, dim3(256), 0, stream, c);
+    else if (need <= 4 || 64 / kSG < 8)
+        hipLaunchKernelGGL((pd_combine_kernel<kCols, (64 / kSG < 4 ? 64 / kSG : 4)>), grid, dim3(256), 0, stream, c);
+    else
+        hipLaunchKernelGGL((pd_combine_kernel<kCols, (64 / kSG < 8 ? 64 / kSG : 8)>), grid, dim3(256), 0, stream, c);
+}
+
 hipError_t launch_combine(const LaunchArgs& x, hipStream_t stream) {
     CombineParams c;
     c.part_o = x.part_o;
@@ -1064,9 +1081,9 @@ hipError_t launch_combine(const LaunchArgs& x, hipStream_t stream) {
     // Few rows: a quarter row per workgroup for parallelism; many rows: half rows, fewer
     // workgroups (config 3, 768 rows: 31.3 -> 29.7 us per layer; 24 rows: 12.2 against 12.6).
     if ((int64_t)x.num_tokens * x.heads_q <= 256)
-        hipLaunchKernelGGL((pd_combine_kernel<16>), dim3(x.num_tokens, x.heads_q, 4), dim3(256), 0, stream, c);
+        launch_combine_cols<16>(c, dim3(x.num_tokens, x.heads_q, 4), stream);
     else
-        hipLaunchKernelGGL((pd_combine_kernel<32>), dim3(x.num_tokens, x.heads_q, 2), dim3(256), 0, stream, c);
+        launch_combine_cols<32>(c, dim3(x.num_tokens, x.heads_q, 2), stream);
     return hipGetLastError();
 }
 
