@@ -82,6 +82,12 @@ template <bool kFast, bool kExact, bool kSplit>
 __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaParams a) {
     constexpr int kLdsRaw = 0;
     constexpr int kLdsH = kLdsRaw + kFaRaw * kSlot;
+    // The unsplit default instance addresses its widening stores from bases held per tile (see
+    // widen_load), starts its row sums from the first term and forms P' by v_fma_mix; the split
+    // and exact instances measured slower with these (the split one 4.14 -> 4.23 ms at 2,560
+    // tokens x 4 splits, fma_mix being the part that costs it) and keep per-store addresses and
+    // a multiply and a conversion for P'.
+    constexpr bool kPinned = !kExact && !kSplit;
     constexpr int kLdsBt = kLdsH + 2 * kFaHBuf;
     constexpr int kLdsBytes = kLdsBt + kFaBt * 4;
     static_assert(kLdsBytes <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
@@ -256,11 +262,11 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
     };
     auto widen_load = [&](int n, WidenRegs& r) __attribute__((always_inline)) {
         // The fp16 buffers lie above 64 KiB, beyond the 16-bit offset of an LDS instruction: the
-        // default instance forms the destinations once per tile and holds them opaque, so that
-        // every store carries only its small offset as an immediate. The exact instance, which
-        // holds more registers across the products, measured slower carrying them (4.03 -> 4.18
-        // ms at config 5) and addresses each store from the buffer base.
-        if constexpr (!kExact) {
+        // unsplit default instance forms the destinations once per tile and holds them opaque,
+        // so that every store carries only its small offset as an immediate (the exact instance,
+        // which holds more registers across the products, measured slower carrying them: 4.03 ->
+        // 4.18 ms at config 5).
+        if constexpr (kPinned) {
             r.h = hbuf(n) + 16 * l;
             r.hs = hbuf(n) + kFaHK + kFaHV + 4 * l;
             asm("" : "+v"(r.h), "+v"(r.hs));
@@ -283,10 +289,7 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
     };
     // piece j of 0..9: K halves 0..3, V blocks 4..7, the tail block 8, the scales 9
     auto widen_store = [&](int n, const WidenRegs& r, int j) __attribute__((always_inline)) {
-        lds_u8* const h = kExact ? hbuf(n) + 16 * l : r.h;
-        lds_u8* const hk = kExact ? h + 4096 * w : r.hk;
-        lds_u8* const hv = kExact ? h + kFaHK + 1024 * w : r.hv;
-        lds_u8* const hs = kExact ? hbuf(n) + kFaHK + kFaHV + 4 * l : r.hs;
+        lds_u8* H = hbuf(n);
         if (j < 4) {
             const int u = j >> 1, hh = j & 1;
             half8_t kf;
@@ -294,28 +297,32 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
                 kf = hh == 0 ? widen_i8x8_exact(r.kr[u].x, r.kr[u].y) : widen_i8x8_exact(r.kr[u].z, r.kr[u].w);
             else
                 kf = hh == 0 ? widen_i8x8(r.kr[u].x, r.kr[u].y) : widen_i8x8(r.kr[u].z, r.kr[u].w);
-            *(lds_half8*)(hk + (2 * hh + u) * 1024) = kf;  // block (2 w + hh) * 2 + u
+            lds_u8* const d = kPinned ? r.hk + (2 * hh + u) * 1024 : H + ((2 * w + hh) * 2 + u) * 1024 + 16 * l;
+            *(lds_half8*)d = kf;
         } else if (j < 8) {
             // kExact: V widened exactly (no bias), so the fp32 P.V accumulators hold only the
             // products' own sums; else with the bias, removed per row at the end
             const int2_t vr = r.vr[j - 4];
-            *(lds_half8*)(hv + 4096 * (j - 4)) =  // block w + 4 (j - 4)
+            lds_u8* const d = kPinned ? r.hv + 4096 * (j - 4) : H + kFaHK + (w + 4 * (j - 4)) * 1024 + 16 * l;
+            *(lds_half8*)d =
                 kExact ? widen_i8x8_exact((unsigned)vr.x, (unsigned)vr.y) : widen_i8x8((unsigned)vr.x, (unsigned)vr.y);
         } else if (j == 8) {
             // rows 12..15 of the tail block are the v_scale bytes. kExact: the O^T rows they feed
             // (lane group 3 of accumulator block 16) are never stored. Else they are widened from
             // 0 to exactly 1152, so those rows accumulate 1152 * sum of P', the bias to remove
             if constexpr (kExact) {
-                *(lds_half8*)(h + kFaHK + 16 * 1024) = widen_i8x8_exact((unsigned)r.vr[4].x, (unsigned)r.vr[4].y);
+                *(lds_half8*)(H + kFaHK + 16 * 1024 + 16 * l) = widen_i8x8_exact((unsigned)r.vr[4].x, (unsigned)r.vr[4].y);
             } else {
                 const int2_t vt = li >= 12 ? int2_t{0, 0} : r.vr[4];
-                *(lds_half8*)(h + kFaHK + 16 * 1024) = widen_i8x8((unsigned)vt.x, (unsigned)vt.y);
+                lds_u8* const d = kPinned ? r.h + kFaHK + 16 * 1024 : H + kFaHK + 16 * 1024 + 16 * l;
+                *(lds_half8*)d = widen_i8x8((unsigned)vt.x, (unsigned)vt.y);
             }
         } else {
             // k_scale * scale * log2(e) [32] then v_scale [32]; keys past seq_len may hold garbage
             // scales (even NaN): v_scale 0 makes their P' 0
             const bool dead = l >= 32 && n * kTile + sr >= hi;
-            *(lds_float*)hs = dead ? 0.f : r.sc * sc_mul;
+            lds_float* const d = kPinned ? (lds_float*)r.hs : (lds_float*)(H + kFaHK + kFaHV + 4 * l);
+            *d = dead ? 0.f : r.sc * sc_mul;
         }
     };
     auto widen = [&](int n) __attribute__((always_inline)) {
@@ -435,12 +442,12 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
         half8_t pop[kFaRB], plo[kFaRB];
 #pragma unroll
         for (int rb = 0; rb < kFaRB; ++rb) {
-            float psum;
+            float psum = 0.f;
 #pragma unroll
             for (int e = 0; e < 8; e += 2) {
                 const float p0 = __builtin_amdgcn_exp2f(sv[rb][e]);
                 const float p1 = __builtin_amdgcn_exp2f(sv[rb][e + 1]);
-                psum = e == 0 ? p0 : psum + p0;
+                psum = e == 0 && kPinned ? p0 : psum + p0;
                 psum += p1;
                 if constexpr (kExact) {
                     half2_t ph, pl;
@@ -449,11 +456,14 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
                     pop[rb][e + 1] = ph.y;
                     plo[rb][e] = pl.x;
                     plo[rb][e + 1] = pl.y;
-                } else {
+                } else if constexpr (kPinned) {
                     // p * v_scale rounded once to fp16 (v_fma_mix with a zero addend: one
                     // instruction per value, where a multiply and a packed conversion take 1.5)
                     pop[rb][e] = (_Float16)__builtin_fmaf(p0, vs[e], 0.f);
                     pop[rb][e + 1] = (_Float16)__builtin_fmaf(p1, vs[e + 1], 0.f);
+                } else {
+                    pop[rb][e] = (_Float16)(p0 * vs[e]);
+                    pop[rb][e + 1] = (_Float16)(p1 * vs[e + 1]);
                 }
             }
             l_run[rb] += psum;
