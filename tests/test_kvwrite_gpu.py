@@ -1,6 +1,7 @@
 """GPU parity of the KV-cache writer (pth_cache_write) against the CPU oracle: bit-exact cache
 bytes for fp16, bf16 and fp32 inputs (including values on exact rounding ties, all-zero rows and
-rows that clamp), HND and NHD, block sizes 16, 1584 and 1, padding slots untouched; and decode
+rows that clamp), HND and NHD, block sizes 16, 1584 and 1, padding slots untouched, through both
+of its kernels (one row per wave below 4,096 rows, four rows per wave from there); and decode
 over a GPU-written cache equals decode over the oracle-written one bit for bit.
 """
 import sys
@@ -42,12 +43,9 @@ def make_inputs(T, hkv, dtype, seed):
     return k.to(dtype), v.to(dtype)
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("bs,layout", [(16, "HND"), (16, "NHD"), (1584, "HND"), (1, "NHD")])
-def test_bit_exact_against_oracle(dtype, bs, layout):
-    T, hkv = 300, 4
+def write_and_compare(T, hkv, dtype, bs, layout, seed):
     nblk = (T + bs - 1) // bs + 3
-    k, v = make_inputs(T, hkv, dtype, seed=bs + T)
+    k, v = make_inputs(T, hkv, dtype, seed=seed)
     g = torch.Generator().manual_seed(9)
     slots = torch.randperm(nblk * bs, generator=g)[:T].to(torch.int64)
     slots[::17] = -1                          # padding tokens
@@ -55,10 +53,25 @@ def test_bit_exact_against_oracle(dtype, bs, layout):
     ref.kv.copy_(torch.randint(-128, 128, ref.kv.shape, dtype=torch.int8, generator=g))
     dev = kvc.clone_cache(ref, "cuda")
     kvw.write_rows(k.float(), v.float(), ref.key_cache, ref.value_cache, ref.k_scale, ref.v_scale, slots)
-    say(f"cache write dtype={dtype} bs={bs} layout={layout}")
+    say(f"cache write T={T} hkv={hkv} dtype={dtype} bs={bs} layout={layout}")
     pth_dec.cache_write(k.cuda(), v.cuda(), dev.key_cache, dev.value_cache, dev.k_scale, dev.v_scale, slots.cuda())
     torch.cuda.synchronize()
     assert torch.equal(dev.kv.cpu(), ref.kv)
+
+
+# 300 x 4 rows take the kernel with one row per wave, 1,100 x 4 the one with four rows per wave
+# (calls of at least 4,096 rows)
+@pytest.mark.parametrize("T", [300, 1100])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("bs,layout", [(16, "HND"), (16, "NHD"), (1584, "HND"), (1, "NHD")])
+def test_bit_exact_against_oracle(T, dtype, bs, layout):
+    write_and_compare(T, 4, dtype, bs, layout, seed=bs + T)
+
+
+@pytest.mark.parametrize("T,hkv", [(819, 5), (1024, 4)])
+def test_rows_per_wave_switch(T, hkv):
+    """819 x 5 = 4,095 rows take one row per wave, 1,024 x 4 = 4,096 four rows per wave."""
+    write_and_compare(T, hkv, torch.float16, 16, "NHD", seed=T)
 
 
 def test_decode_over_gpu_written_cache_is_bit_identical():
