@@ -287,7 +287,8 @@ def test_cache_write_random(i):
     qkv_d = qkv.cuda()
     k = qkv_d[:, hq * 256:(hq + hkv) * 256].view(T, hkv, 256)
     v = qkv_d[:, (hq + hkv) * 256:].view(T, hkv, 256)
-    assert not k.is_contiguous() and k.stride(0) == (hq + 2 * hkv) * 256
+    # (a view with one token has no meaningful token stride: torch reports it as contiguous)
+    assert T == 1 or (not k.is_contiguous() and k.stride(0) == (hq + 2 * hkv) * 256)
     pth_dec.cache_write(k, v, dev.key_cache, dev.value_cache, dev.k_scale, dev.v_scale, slots.cuda())
     torch.cuda.synchronize()
     assert torch.equal(dev.kv.cpu(), ref.kv)
