@@ -1,8 +1,10 @@
 """GPU parity of the KV-cache writer (pth_cache_write) against the CPU oracle: bit-exact cache
 bytes for fp16, bf16 and fp32 inputs (including values on exact rounding ties, all-zero rows and
-rows that clamp), HND and NHD, block sizes 16, 1584 and 1, padding slots untouched, through both
-of its kernels (one row per wave below 4,096 rows, four rows per wave from there); and decode
-over a GPU-written cache equals decode over the oracle-written one bit for bit.
+rows that clamp, rows whose scale is subnormal), HND and NHD, block sizes 16, 1584 and 1, padding
+slots untouched, through each of its three kernel forms (one row per wave below 4,096 rows, four
+rows per wave from there, and from 16,384 rows four rows per wave quantising through the row's
+inverse scale); and decode over a GPU-written cache equals decode over the oracle-written one bit
+for bit.
 """
 import sys
 
@@ -40,6 +42,15 @@ def make_inputs(T, hkv, dtype, seed):
         row[:near.size] = bits.astype(np.int32).view(np.float32)
         row[255] = 38.1
         k[2, 1] = torch.from_numpy(row)
+    # subnormal scales (float32 and bfloat16 inputs; in float16 these rows underflow to zero): absmax
+    # 1e-37 gives a scale whose inverse overflows to infinity, 127 x 3e-39 one whose inverse is
+    # finite, and a row of subnormal inputs a scale of a few subnormal ulps
+    if T > 4:
+        k[3, 2 % hkv] = torch.randn(256, generator=g) * 1e-37
+        k[3, 2 % hkv, 7] = 1e-37
+        v[3, 2 % hkv] = torch.rand(256, generator=g) * (127 * 3e-39)
+        v[3, 2 % hkv, 9] = -127 * 3e-39
+        k[4, 3 % hkv] = torch.randn(256, generator=g) * 1e-40
     return k.to(dtype), v.to(dtype)
 
 
@@ -60,8 +71,8 @@ def write_and_compare(T, hkv, dtype, bs, layout, seed):
 
 
 # 300 x 4 rows take the kernel with one row per wave, 1,100 x 4 the one with four rows per wave
-# (calls of at least 4,096 rows)
-@pytest.mark.parametrize("T", [300, 1100])
+# (calls of at least 4,096 rows), 4,100 x 4 the one through the inverse scale (at least 16,384)
+@pytest.mark.parametrize("T", [300, 1100, 4100])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("bs,layout", [(16, "HND"), (16, "NHD"), (1584, "HND"), (1, "NHD")])
 def test_bit_exact_against_oracle(T, dtype, bs, layout):

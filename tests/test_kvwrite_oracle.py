@@ -47,6 +47,23 @@ def test_round_trip_bound():
     assert (err <= s[:, None].astype(np.float64) * 0.5 * (1 + 1e-6)).all()
 
 
+def test_subnormal_scales_are_kept():
+    """Rows of absmax ~1e-37 have subnormal scales (1 / scale overflows float32 for most of
+    them): the scale is not flushed to zero, the extremes still map to +-127 and the round-trip
+    bound holds (the scale keeps ~19 significant bits at this size)."""
+    rng = np.random.default_rng(6)
+    x = (rng.standard_normal((40, 256)) * rng.uniform(0.3, 3.0, (40, 1)) * 1e-37).astype(np.float32)
+    q, s = kvw.quantize_rows(x)
+    tiny = np.finfo(np.float32).tiny
+    assert ((s > 0) & (s < tiny)).all()
+    with np.errstate(over="ignore"):
+        assert np.isinf(np.float32(1) / s).any() and np.isfinite(np.float32(1) / s).any()
+    am = np.abs(x).argmax(-1)
+    assert (np.abs(np.take_along_axis(q.astype(np.int32), am[:, None], -1)) == 127).all()
+    err = np.abs(q.astype(np.float64) * s[:, None].astype(np.float64) - x)
+    assert (err <= s[:, None].astype(np.float64) * 0.5 * (1 + 1e-5)).all()
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_agrees_with_the_torch_quantiser(dtype):
     g = torch.Generator().manual_seed(5)
