@@ -11,6 +11,12 @@
  * value_cache is the same storage shifted by 260 bytes; k_scale / v_scale are f32 views
  * [blocks, block_size, Hkv] at +256 / +516 bytes of each row.
  *
+ * Range of the attention entry points (decode and prefill): each key's value weight is formed in
+ * fp16 as p * v_scale * 16 with p <= 16 (the running max lags a row's true max by at most 4 in
+ * log2 units), so v_scale must stay below 255.9, i.e. V rows with absmax below ~32,500. Larger
+ * scales can overflow that weight to infinity. pth_cache_write produces such scales only from
+ * V inputs above ~32,500 in magnitude.
+ *
  * Reference interfaces replaced (paths relative to the 0c33/mi50-vllm-lab tree):
  *   pth_dec_launch             <- kernels/pth_dec/pth_dec.cu:285-314 (same signature)
  *   pth_dec_launch_window      <- same, plus the window / non-causal rule of
