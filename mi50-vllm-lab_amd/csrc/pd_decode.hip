@@ -9,7 +9,10 @@
 //   The keys a sequence can see, [lo, seq_len), are cut into 32-key tiles aligned to
 //   multiples of 32; split s owns a contiguous run of tiles and wave w of that split takes
 //   every 4th tile. All R = q_len * G query rows of the GQA group (24 for MTP, 48 for
-//   DFlash2) are held as 16-row blocks, so one read of a K/V tile serves every row.
+//   DFlash2) are held as 16-row blocks, so one read of a K/V tile serves every row. Windowed
+//   groups of more than 16 rows are instead sliced into 16-row workgroups (grid z = slice x
+//   sequence) when nsplit x Hkv x num_seqs x slices fits the CUs: a windowed row sees few tiles,
+//   so the slices' repeated reads of them cost less than the split partials they save.
 //
 // Memory path: HBM -> LDS by DMA (global_load_lds_dwordx4), double-buffered per wave, no VGPR
 //   holding data in flight. A tile is 17 DMA instructions of 1 KiB: 8 for K (4 rows x 256
@@ -150,7 +153,12 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     static_assert(kLdsBytes <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
     __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
 
-    const int s = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    // grid z = row slice x sequence: with rslices > 1 the workgroup takes rows [row0, row0 + 16 NRB)
+    // of its GQA group, and the group's other slices read the same tiles
+    const int s = blockIdx.x, g = blockIdx.y;
+    const int rs = a.rslices > 1 ? (int)blockIdx.z / a.num_seqs : 0;
+    const int b = (int)blockIdx.z - rs * a.num_seqs;
+    const int row0 = 16 * NRB * rs;
     const int tid = threadIdx.x, l = tid & 63, lg = l >> 4, li = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, uniform by construction
 
@@ -169,7 +177,8 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     if (q_len <= 0 || seq_len <= 0) return;
     const int ql = min(q_len, a.qmax);
     const int G = a.G;
-    const int R = ql * G;
+    const int R = min(16 * NRB, ql * G - row0);  // rows of this workgroup: group rows row0 + [0, R)
+    if (R <= 0) return;                          // a slice past the sequence's rows
     const int ctx0 = seq_len - q_len;  // absolute position of query token 0
     const int lo = a.window > 0 ? max(0, ctx0 - a.window + 1) : 0;
     const int hi = seq_len;
@@ -189,7 +198,7 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     const bool empty = interleave ? kWaves * s >= ntiles : tb >= te;
 
     auto prow = [&](int r) -> int64_t {  // partial row index of query row r
-        const int i = r / G, hh = r - i * G;
+        const int i = (row0 + r) / G, hh = (row0 + r) - i * G;
         return ((int64_t)(q0 + i) * a.Hq + (g * G + hh)) * a.nseg + s;
     };
 
@@ -238,7 +247,7 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
     for (int rb = 0; rb < NRB; ++rb) {
         const int r = 16 * rb + li;
         rvalid[rb] = r < R;
-        const int qi = r / G, qh = r - (r / G) * G;
+        const int qi = (row0 + r) / G, qh = (row0 + r) - qi * G;
         rpos[rb] = ctx0 + qi;
         if constexpr (kEarly) continue;
         const _Float16* qrow =
@@ -307,7 +316,7 @@ __global__ void __launch_bounds__(kThreads, 1) pd_partial_kernel(const PartialPa
         //     waves, and the raw block-table entries of each wave's blocks
         const int nq = (R + 1) / 2;
         for (int i = w; i < nq; i += kWaves) {
-            const int r = min(2 * i + (l >> 5), R - 1);
+            const int r = row0 + min(2 * i + (l >> 5), R - 1);
             const int qi = r / G, qh = r - qi * G;
             const _Float16* qrow = a.q + (int64_t)(q0 + qi) * a.q_st + (int64_t)(g * G + qh) * kDim;
             const int qdst = kQInSlots ? (2 * i / 16) * kWaveLds + kSlot + kImgV + (2 * i % 16) * (2 * kDim)
@@ -1007,6 +1016,20 @@ hipError_t check_args(const LaunchArgs& x, bool strict_reference) {
     return hipSuccess;
 }
 
+// Compute units of the device a stream belongs to (looked up once per device; 0 if unknown).
+static int compute_units(hipStream_t stream) {
+    constexpr int kDevices = 64;
+    static std::atomic<int> cached[kDevices];
+    int dev = -1;
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess || dev < 0 || dev >= kDevices) return 0;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        cached[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
 template <int NRB>
 hipError_t launch_partial_nrb(const PartialParams& p, dim3 grid, hipStream_t stream, bool fast) {
     const dim3 block(kThreads);
@@ -1043,9 +1066,19 @@ hipError_t launch_partial(const LaunchArgs& x, hipStream_t stream) {
     p.causal = x.causal ? 1 : 0;
     p.bs_shift = (x.block_size & (x.block_size - 1)) == 0 ? __builtin_ctz((unsigned)x.block_size) : -1;
     const int rows = x.qmax * p.G;
-    const dim3 grid(x.nsplit, x.heads_kv, x.num_seqs);
+    const int nrb = rows <= 16 ? 1 : rows <= 32 ? 2 : 3;
+    // Windowed groups of more than 16 rows are sliced into 16-row workgroups when that still
+    // fits one round of workgroups: a windowed row sees few tiles, so each slice re-reading them
+    // costs less than the rounds of split partials it saves (4 x 8 rows over 2,048-key windows:
+    // 23.8 -> 19.3 us per layer at 5 splits of 3 slices against 16 unsliced splits).
+    p.num_seqs = x.num_seqs;
+    p.rslices = nrb > 1 && x.window > 0 && x.window <= kSliceWindow &&
+                        (int64_t)x.nsplit * x.heads_kv * x.num_seqs * nrb <= compute_units(stream)
+                    ? nrb
+                    : 1;
+    const dim3 grid(x.nsplit, x.heads_kv, x.num_seqs * p.rslices);
     const bool fast = fast_block_table(x.block_size, x.k_ss);
-    if (rows <= 16) return launch_partial_nrb<1>(p, grid, stream, fast);
+    if (rows <= 16 || p.rslices > 1) return launch_partial_nrb<1>(p, grid, stream, fast);
     if (rows <= 32) return launch_partial_nrb<2>(p, grid, stream, fast);
     return launch_partial_nrb<3>(p, grid, stream, fast);
 }

@@ -12,6 +12,7 @@ namespace pd {
 
 constexpr int kDim = 256;             // head dim (the only one the cache row layout allows)
 constexpr int kMaxRowBlocks = 3;      // decode: up to 48 query rows per kv head
+constexpr int kSliceWindow = 4096;    // decode: largest sliding window whose row groups are sliced
 
 // Prefill workgroup shape: kFaWaves waves of kFaRB 16-row blocks, so a workgroup takes
 // kFaRows / G query tokens of one sequence and all G heads of one kv head.
@@ -42,6 +43,8 @@ struct PartialParams {
     int window;              // > 0: sliding window, else none
     int causal;
     int bs_shift;            // log2(block_size) if it is a power of two, else -1
+    int num_seqs;
+    int rslices;             // workgroups per (sequence, kv head, split), each 16 NRB of the rows
 };
 
 // Split-K decode, log-sum-exp merge of the partials (pd_combine_kernel).

@@ -79,6 +79,29 @@ SPLIT_FIXED_US, SPLIT_TILE_US, SPLIT_EMPTY_US = 12.0, 3.3, 2.0
 COMBINE_US_PER_MB = 0.25
 PARTIAL_ROW_BYTES = 1032
 
+# The operator runs a windowed GQA group of more than 16 rows as 16-row slices, one workgroup
+# each, when splits x kv heads x sequences x slices fits the CUs and the window is at most
+# SLICE_WINDOW keys (pd_decode.hip, launch_partial). Measured on MI355X (24 q / 4 kv heads, us per
+# layer, sliced at the largest such split count against the best unsliced count): 4 x 8 rows
+# over 2,048-key windows 19.7 (5) against 24.1 (16); 1 x 8 rows 13.2 (21) against 17.7 (32);
+# 4 x 4 rows 17.1 (8) against 19.1 (16); 2 x 8 rows over 4,096 keys 19.3 (10) against 25.2 (32);
+# 8 x 8 rows over 1,024 keys 23.1 (2) against 26.8 (8); but 16 x 8 rows 46.8 (1) against
+# 45.3 (4). So that count is taken when it is at least 2.
+SLICE_WINDOW = 4096
+
+
+def sliced_splits(window: int, max_q: int, group: int, num_kv_heads: int, num_seqs: int, cus: int,
+                  cap: int) -> int:
+    """The split count at which the operator slices this windowed batch into one round of 16-row
+    workgroups, or 0 when it would not (no window or a longer one, at most 16 rows per group,
+    or fewer than 2 splits would fit)."""
+    rows = max(1, max_q) * group
+    if window <= 0 or window > SLICE_WINDOW or rows <= 16:
+        return 0
+    slices = -(-rows // 16)
+    s = min(cap, cus // max(1, num_kv_heads * num_seqs * slices))
+    return s if s >= 2 else 0
+
 
 def decode_splits(nseg: int, window: int, num_kv_heads: int, num_seqs: int, device, seq_lens_host=None,
                   max_q: int = 1, num_q_heads: Optional[int] = None) -> int:
@@ -90,9 +113,15 @@ def decode_splits(nseg: int, window: int, num_kv_heads: int, num_seqs: int, devi
     6 q heads per kv head when not given). Few splits for many sequences, many for one long
     sequence. Without the lengths: a sliding window bounds every sequence to about window + qmax
     keys, so the grid is sized to one workgroup per CU; otherwise the cap (the reference's
-    rule)."""
+    rule). Before either: windowed groups of more than 16 rows take the count at which the
+    operator slices them into one round of 16-row workgroups (sliced_splits), when that is at
+    least 2."""
     cap = max(1, min(PTH_DEC_SPLITS, nseg))
     cus = cu_count(device)
+    group = num_q_heads // num_kv_heads if num_q_heads else 6
+    sliced = sliced_splits(window, max_q, group, num_kv_heads, num_seqs, cus, cap)
+    if sliced:
+        return sliced
     if seq_lens_host is None:
         if window > 0:
             return max(1, min(cap, cus // max(1, num_kv_heads * num_seqs)))

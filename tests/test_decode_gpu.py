@@ -270,6 +270,35 @@ def test_gqa_group_sizes(hq, hkv, qlens):
         assert emax <= 2e-3 and emean <= 2e-4, (ns, emax, emean)
 
 
+@pytest.mark.parametrize("hq,ctxs,qlens,window,causal", [
+    (24, [2048, 9216, 33792, 122880], [8, 8, 8, 8], 2048, False),  # 48 rows: 3 slices
+    (24, [5000, 700, 64], [4, 2, 1], 1000, True),                    # 24 rows: 2 slices, upper ones empty
+    (48, [3000, 40], [4, 1], 4096, True),                            # G = 12, 48 rows, the largest sliced window
+    (24, [6000, 2100], [8, 3], 4097, False),                         # one key past it: never sliced
+])
+def test_windowed_row_slices(hq, ctxs, qlens, window, causal):
+    """Windowed GQA groups of more than 16 rows run as 16-row slices, one workgroup each, when
+    nsplit x heads_kv x num_seqs x slices fits the CUs (here at 1 and 5 splits), and unsliced at
+    64 splits. Every count meets the bar, pages outside the windows are NaN-poisoned, and the
+    slices past a sequence's query rows write nothing."""
+    c = kvc.make_case(ctxs, qlens, num_q_heads=hq, num_kv_heads=HKV, block_size=16, seed=hq + window,
+                      window=window, causal=causal, poison=True)
+    ref, written = oracle_of(c)
+    d = c.to("cuda")
+    T = d.num_tokens
+    for ns in (1, 5, 64):
+        say(f"row slices hq={hq} ctxs={ctxs} qlens={qlens} window={window} nsplit={ns}")
+        out = torch.full((T, hq, 256), float("nan"), dtype=torch.float16, device="cuda")
+        po, pm, pl = kvc.partial_buffers(T, hq, NSEG, "cuda")
+        pth_dec.decode(d.q, d.cache.key_cache, d.cache.value_cache, d.cache.k_scale, d.cache.v_scale, d.block_table,
+                       d.seq_lens, d.query_start_loc, out, d.scale, po, pm, pl, d.num_seqs, d.qmax, ns, d.window,
+                       d.causal)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out.float()).all()
+        emax, emean = errors(out, ref, written)
+        assert emax <= 2e-3 and emean <= 2e-4, (ns, emax, emean)
+
+
 def test_padding_tokens_untouched():
     c = kvc.make_case([300, 40], [4, 2], num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=8)
     d = c.to("cuda")

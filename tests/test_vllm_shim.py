@@ -108,10 +108,12 @@ def test_decode_rows_route_to_decode_with_nsplit_cap(ops):
     assert (out == 1).all()
 
 
-@pytest.mark.parametrize("nseqs,nseg,want", [(4, 64, 16), (1, 64, 64), (2, 24, 24), (80, 64, 1)])
+@pytest.mark.parametrize("nseqs,nseg,want", [(4, 64, 8), (1, 64, 32), (2, 24, 16), (2, 12, 12), (80, 64, 1)])
 def test_window_rows_fill_one_round_of_workgroups(ops, nseqs, nseg, want):
-    """With a sliding window the split count is capped at CUs / (kv heads x sequences) (256 CUs
-    on a CPU device): one round of partial workgroups."""
+    """With a sliding window the split count fills one round of partial workgroups (256 CUs on a
+    CPU device). These groups have 4 x 6 = 24 rows, which the operator runs as two 16-row
+    slices: CUs / (kv heads x sequences x 2), while that is at least 2 (80 sequences: the
+    unsliced rule, CUs / (kv heads x sequences), gives 1)."""
     a = impl(sliding_window=(2047, -1))
     q, out, kc = tensors(4 * nseqs)
     m = meta([4] * nseqs, [3000 + 7 * i for i in range(nseqs)], nseg=nseg)
@@ -128,8 +130,26 @@ MEASURED_BEST = [
     ([120004] + [2052] * 7, 4, -1, 32),         # 1993 / 1011 / 519 / 273 / 151 / 91 / 119
     ([61444], 4, -1, 64),                       # config 2 (MTP verify, 61k)
     ([4097], 1, -1, 64),                        # config 1: 15.1 at 16, 13.4 at 32, 12.2 at 64
-    ([2056, 9224, 33800, 122888], 8, 2048, 16),  # config 3: 34.3 at 8, 32.6 at 16, 42.7 at 32
+    ([2056, 9224, 33800, 122888], 8, 2048, 5),   # config 3, sliced: 19.7 at 5; unsliced 25.7 at 8, 24.1 at 16
 ]
+
+
+def test_sliced_splits_rule():
+    """Windowed groups of more than 16 rows: the largest split count at which slices of 16 rows
+    still fill one round of workgroups, if at least 2 (else 0: the makespan model decides)."""
+    ss = shim.sliced_splits
+    assert ss(2048, 8, 6, 4, 4, 256, 64) == 5        # config 3: 48 rows, 3 slices
+    assert ss(2048, 8, 6, 4, 1, 256, 64) == 21
+    assert ss(2048, 4, 6, 4, 4, 256, 64) == 8        # 24 rows, 2 slices
+    assert ss(2048, 8, 6, 4, 16, 256, 64) == 0       # only 1 split would fit
+    assert ss(2048, 8, 6, 4, 1, 256, 16) == 16       # capped at nseg
+    assert ss(4096, 8, 6, 4, 2, 256, 64) == 10
+    assert ss(4097, 8, 6, 4, 2, 256, 64) == 0        # past the sliced windows
+    assert ss(-1, 8, 6, 4, 1, 256, 64) == 0          # no window
+    assert ss(2048, 2, 6, 4, 1, 256, 64) == 0        # 12 rows: one row block, nothing to slice
+    # the model is consulted only when slicing does not apply
+    assert shim.decode_splits(64, 2048, 4, 16, "cpu", [4104] * 16, 8) == \
+        shim.decode_splits(64, 2048, 4, 16, "cpu", [4104] * 16, 8, 24)
 
 
 @pytest.mark.parametrize("lens,qmax,window,best", MEASURED_BEST)
