@@ -11,8 +11,9 @@
 //   every 4th tile. All R = q_len * G query rows of the GQA group (24 for MTP, 48 for
 //   DFlash2) are held as 16-row blocks, so one read of a K/V tile serves every row. Windowed
 //   groups of more than 16 rows are instead sliced into 16-row workgroups (grid z = slice x
-//   sequence) when nsplit x Hkv x num_seqs x slices fits the CUs: a windowed row sees few tiles,
-//   so the slices' repeated reads of them cost less than the split partials they save.
+//   sequence) when nsplit x Hkv x num_seqs x slices fits the CUs and num_seqs x window is at most
+//   16,384 keys: then the slices' repeated reads of the tiles cost less than the split partials
+//   they save.
 //
 // Memory path: HBM -> LDS by DMA (global_load_lds_dwordx4), double-buffered per wave, no VGPR
 //   holding data in flight. A tile is 17 DMA instructions of 1 KiB: 8 for K (4 rows x 256
@@ -1068,11 +1069,12 @@ hipError_t launch_partial(const LaunchArgs& x, hipStream_t stream) {
     const int rows = x.qmax * p.G;
     const int nrb = rows <= 16 ? 1 : rows <= 32 ? 2 : 3;
     // Windowed groups of more than 16 rows are sliced into 16-row workgroups when that still
-    // fits one round of workgroups: a windowed row sees few tiles, so each slice re-reading them
-    // costs less than the rounds of split partials it saves (4 x 8 rows over 2,048-key windows:
-    // 23.8 -> 19.3 us per layer at 5 splits of 3 slices against 16 unsliced splits).
+    // fits one round of workgroups and the batch's windows hold at most kSliceKeys keys: then
+    // each slice re-reading the tiles costs less than the split partials it saves (4 x 8 rows
+    // over 2,048-key windows: 23.8 -> 19.3 us per layer at 5 splits of 3 slices against 16
+    // unsliced splits; past kSliceKeys, e.g. 4 x 8 rows over 8,192 keys, slicing lost).
     p.num_seqs = x.num_seqs;
-    p.rslices = nrb > 1 && x.window > 0 && x.window <= kSliceWindow &&
+    p.rslices = nrb > 1 && x.window > 0 && (int64_t)x.window * x.num_seqs <= kSliceKeys &&
                         (int64_t)x.nsplit * x.heads_kv * x.num_seqs * nrb <= compute_units(stream)
                     ? nrb
                     : 1;

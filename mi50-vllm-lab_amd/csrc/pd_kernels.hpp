@@ -12,7 +12,7 @@ namespace pd {
 
 constexpr int kDim = 256;             // head dim (the only one the cache row layout allows)
 constexpr int kMaxRowBlocks = 3;      // decode: up to 48 query rows per kv head
-constexpr int kSliceWindow = 4096;    // decode: largest sliding window whose row groups are sliced
+constexpr int64_t kSliceKeys = 16384; // decode: largest sequences x window whose row groups are sliced
 
 // Prefill workgroup shape: kFaWaves waves of kFaRB 16-row blocks, so a workgroup takes
 // kFaRows / G query tokens of one sequence and all G heads of one kv head.

@@ -80,23 +80,25 @@ COMBINE_US_PER_MB = 0.25
 PARTIAL_ROW_BYTES = 1032
 
 # The operator runs a windowed GQA group of more than 16 rows as 16-row slices, one workgroup
-# each, when splits x kv heads x sequences x slices fits the CUs and the window is at most
-# SLICE_WINDOW keys (pd_decode.hip, launch_partial). Measured on MI355X (24 q / 4 kv heads, us per
-# layer, sliced at the largest such split count against the best unsliced count): 4 x 8 rows
-# over 2,048-key windows 19.7 (5) against 24.1 (16); 1 x 8 rows 13.2 (21) against 17.7 (32);
-# 4 x 4 rows 17.1 (8) against 19.1 (16); 2 x 8 rows over 4,096 keys 19.3 (10) against 25.2 (32);
-# 8 x 8 rows over 1,024 keys 23.1 (2) against 26.8 (8); but 16 x 8 rows 46.8 (1) against
-# 45.3 (4). So that count is taken when it is at least 2.
-SLICE_WINDOW = 4096
+# each, when splits x kv heads x sequences x slices fits the CUs and sequences x window is at
+# most SLICE_KEYS (pd_decode.hip, launch_partial). Measured on MI355X (24 q / 4 kv heads, us per
+# layer, sliced at the best such split count against the best unsliced count): 4 x 8 rows over
+# 2,048-key windows 19.7 (5) against 24.1 (16); 1 x 8 rows 13.2 (21) against 17.7 (32); 4 x 4
+# rows 17.1 (8) against 19.1 (16); 2 x 8 rows over 4,096 keys 19.3 (10) against 25.2 (32);
+# 8 x 8 rows over 1,024 keys 23.1 (2) against 26.8 (8); 1 x 8 rows over 8,192 keys 19.0 (21)
+# against 24.8 (32), over 16,384 keys 24.9 (21) against 27.9 (64). Past SLICE_KEYS it lost: 4 x 8
+# rows over 8,192 keys 41.4 (4) against 34.4 (16), 16 x 8 rows over 2,048 keys 46.8 (1) against
+# 45.3 (4). The largest fitting count is taken when it is at least 2.
+SLICE_KEYS = 16384
 
 
 def sliced_splits(window: int, max_q: int, group: int, num_kv_heads: int, num_seqs: int, cus: int,
                   cap: int) -> int:
     """The split count at which the operator slices this windowed batch into one round of 16-row
-    workgroups, or 0 when it would not (no window or a longer one, at most 16 rows per group,
-    or fewer than 2 splits would fit)."""
+    workgroups, or 0 when it would not (no window, sequences x window above SLICE_KEYS, at most
+    16 rows per group, or fewer than 2 splits would fit)."""
     rows = max(1, max_q) * group
-    if window <= 0 or window > SLICE_WINDOW or rows <= 16:
+    if window <= 0 or window * max(1, num_seqs) > SLICE_KEYS or rows <= 16:
         return 0
     slices = -(-rows // 16)
     s = min(cap, cus // max(1, num_kv_heads * num_seqs * slices))

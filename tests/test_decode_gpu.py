@@ -273,13 +273,13 @@ def test_gqa_group_sizes(hq, hkv, qlens):
 @pytest.mark.parametrize("hq,ctxs,qlens,window,causal", [
     (24, [2048, 9216, 33792, 122880], [8, 8, 8, 8], 2048, False),  # 48 rows: 3 slices
     (24, [5000, 700, 64], [4, 2, 1], 1000, True),                    # 24 rows: 2 slices, upper ones empty
-    (48, [3000, 40], [4, 1], 4096, True),                            # G = 12, 48 rows, the largest sliced window
-    (24, [6000, 2100], [8, 3], 4097, False),                         # one key past it: never sliced
+    (48, [9000, 40], [4, 1], 8192, True),                            # G = 12, 48 rows, 2 x 8,192: the largest sliced
+    (24, [9000, 2100], [8, 3], 8193, False),                         # 2 x 8,193 keys: never sliced
 ])
 def test_windowed_row_slices(hq, ctxs, qlens, window, causal):
     """Windowed GQA groups of more than 16 rows run as 16-row slices, one workgroup each, when
-    nsplit x heads_kv x num_seqs x slices fits the CUs (here at 1 and 5 splits), and unsliced at
-    64 splits. Every count meets the bar, pages outside the windows are NaN-poisoned, and the
+    nsplit x heads_kv x num_seqs x slices fits the CUs (here at 1 and 5 splits) and num_seqs x
+    window is at most 16,384 keys, and unsliced at 64 splits. Every count meets the bar, pages outside the windows are NaN-poisoned, and the
     slices past a sequence's query rows write nothing."""
     c = kvc.make_case(ctxs, qlens, num_q_heads=hq, num_kv_heads=HKV, block_size=16, seed=hq + window,
                       window=window, causal=causal, poison=True)

@@ -144,7 +144,10 @@ def test_sliced_splits_rule():
     assert ss(2048, 8, 6, 4, 16, 256, 64) == 0       # only 1 split would fit
     assert ss(2048, 8, 6, 4, 1, 256, 16) == 16       # capped at nseg
     assert ss(4096, 8, 6, 4, 2, 256, 64) == 10
-    assert ss(4097, 8, 6, 4, 2, 256, 64) == 0        # past the sliced windows
+    assert ss(8192, 8, 6, 4, 2, 256, 64) == 10       # 2 x 8,192 = 16,384 keys: still sliced
+    assert ss(8193, 8, 6, 4, 2, 256, 64) == 0        # past 16,384 keys of windows
+    assert ss(16384, 8, 6, 4, 1, 256, 64) == 21
+    assert ss(8192, 8, 6, 4, 4, 256, 64) == 0        # 4 x 8,192: measured slower sliced
     assert ss(-1, 8, 6, 4, 1, 256, 64) == 0          # no window
     assert ss(2048, 2, 6, 4, 1, 256, 64) == 0        # 12 rows: one row block, nothing to slice
     # the model is consulted only when slicing does not apply
