@@ -387,6 +387,44 @@ def test_hip_graph_capture_and_replay():
         assert torch.equal(got.view(torch.int16), out.view(torch.int16))
 
 
+def test_hip_graph_of_sliced_rows():
+    """The windowed 4 x 8-row batch at 5 splits (three 16-row slices per group) captured in a HIP
+    graph: six replays with new queries, each bit-equal to an eager call on the same inputs."""
+    c = baseline_case(3).to("cuda")
+    T = c.num_tokens
+    out = torch.zeros((T, HQ, 256), dtype=torch.float16, device="cuda")
+    po, pm, pl = kvc.partial_buffers(T, HQ, NSEG, "cuda")
+    q_static = c.q.clone()
+
+    def run():
+        pth_dec.decode(q_static, c.cache.key_cache, c.cache.value_cache, c.cache.k_scale, c.cache.v_scale,
+                       c.block_table, c.seq_lens, c.query_start_loc, out, c.scale, po, pm, pl, c.num_seqs, 8, 5,
+                       c.window, c.causal)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    torch.cuda.synchronize()
+    g = torch.Generator(device="cuda").manual_seed(5)
+    for rep in range(6):
+        q_static.copy_(torch.randn(q_static.shape, device="cuda", generator=g).half())
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        out.zero_()
+        run()
+        torch.cuda.synchronize()
+        say(f"sliced graph replay {rep}")
+        assert torch.isfinite(got.float()).all()
+        assert torch.equal(got.view(torch.int16), out.view(torch.int16))
+
+
 def test_config4_graph_replayed_1000_times():
     """Config 4 as specified: the long-context call (200,000 keys, 1 % outlier rows) captured once in
     a HIP graph and replayed 1,000 times. Every 250th replay is compared with the eager call (bit
