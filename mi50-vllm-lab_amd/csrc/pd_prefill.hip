@@ -96,8 +96,8 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
     // Workgroups are dispatched to the 8 XCDs round robin (linear id L to XCD L % 8), and each XCD
     // has its own L2. Every query tile of a (sequence, kv head) streams the same keys, so the
     // logical workgroup index (query tile fastest) is laid out XCD by XCD: XCD x takes a
-    // contiguous range of it, and the query tiles sharing a kv head mostly share an L2 (config 5:
-    // each kv head's 64 query tiles on two XCDs).
+    // contiguous range of it, and the query tiles sharing a kv head mostly share an L2 (a 2,048-token
+    // chunk at 24 q / 4 kv heads: each kv head's 64 query tiles on two XCDs).
     const unsigned nx = gridDim.x, ny = gridDim.y, nwg = nx * ny * gridDim.z;
     const unsigned lin = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
     const unsigned xcd = lin % 8u;
@@ -265,7 +265,7 @@ __global__ void __launch_bounds__(kFaWaves * 64, 1) pd_prefill_kernel(const FaPa
         // unsplit default instance forms the destinations once per tile and holds them opaque,
         // so that every store carries only its small offset as an immediate (the exact instance,
         // which holds more registers across the products, measured slower carrying them: 4.03 ->
-        // 4.18 ms at config 5).
+        // 4.18 ms for a 2,048-token chunk over 61,440 cached keys).
         if constexpr (kPinned) {
             r.h = hbuf(n) + 16 * l;
             r.hs = hbuf(n) + kFaHK + kFaHV + 4 * l;

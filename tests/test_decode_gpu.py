@@ -2,8 +2,9 @@
 
 Cases follow kernels/pth_dec/test_dec.py:120-140 (the reference's 15 cases at 1, 7, 64 and 128
 splits, its tolerance max-abs < 4e-3, NaN-initialised outputs) re-shaped to the full model on
-one GPU (24 q heads / 4 kv heads), plus the workloads of the north-star configs at full size
-with the stated tolerance (max-abs <= 2e-3, mean-abs <= 2e-4 on fp16 outputs), the NaN-poisoned
+one GPU (24 q heads / 4 kv heads), plus the benchmark decode workloads at full size (single
+token at 4k, MTP verify at 61k, windowed 4 x 8 rows, 200k keys with outlier rows) with the stated
+tolerance (max-abs <= 2e-3, mean-abs <= 2e-4 on fp16 outputs), the NaN-poisoned
 freed-page test (bit-exact), bit-exact invariance to the physical page layout, and HIP-graph
 capture and replay.
 """
@@ -84,7 +85,9 @@ def test_reference_cases(ctxs, qlens, nhd, qnc):
 
 
 def baseline_case(n):
-    """The workloads of the five north-star configs (1-4 here; 5 is the prefill kernel)."""
+    """The benchmark decode workloads: 1 single token over 4,096 keys, 2 MTP verify (4 tokens)
+    over 61,440 keys, 3 four windowed sequences of 8 non-causal tokens (2,048-key window, freed
+    pages poisoned), 4 four tokens over 200,000 keys with 1 % outlier rows."""
     s = 1000 + n
     if n == 1:
         return kvc.make_case([4096], [1], num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=s)
@@ -455,7 +458,7 @@ def test_config4_graph_replayed_1000_times():
         graph.replay()
         if rep % 250 == 0:
             torch.cuda.synchronize()
-            say(f"config 4 graph replay {rep}")
+            say(f"200k-key graph replay {rep}")
             assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), rep
             out.zero_()
             torch.cuda.synchronize()

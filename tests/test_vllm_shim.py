@@ -128,9 +128,9 @@ MEASURED_BEST = [
     ([8196] * 16, 4, -1, 4),                    # 171 / 98 / 72 / 83 / 103 / 141 / 202
     ([4097] * 64, 1, -1, 1),                    # 124 / 124 / 133 / 159 / 203 / 271 / 411
     ([120004] + [2052] * 7, 4, -1, 32),         # 1993 / 1011 / 519 / 273 / 151 / 91 / 119
-    ([61444], 4, -1, 64),                       # config 2 (MTP verify, 61k)
-    ([4097], 1, -1, 64),                        # config 1: 15.1 at 16, 13.4 at 32, 12.2 at 64
-    ([2056, 9224, 33800, 122888], 8, 2048, 5),   # config 3, sliced: 19.7 at 5; unsliced 25.7 at 8, 24.1 at 16
+    ([61444], 4, -1, 64),                       # MTP verify, 4 tokens over 61k
+    ([4097], 1, -1, 64),                        # one token over 4k: 15.1 at 16, 13.4 at 32, 12.2 at 64
+    ([2056, 9224, 33800, 122888], 8, 2048, 5),   # 4 x 8 windowed rows, sliced: 19.7 at 5; unsliced 25.7 at 8, 24.1 at 16
 ]
 
 
@@ -138,7 +138,7 @@ def test_sliced_splits_rule():
     """Windowed groups of more than 16 rows: the largest split count at which slices of 16 rows
     still fill one round of workgroups, if at least 2 (else 0: the makespan model decides)."""
     ss = shim.sliced_splits
-    assert ss(2048, 8, 6, 4, 4, 256, 64) == 5        # config 3: 48 rows, 3 slices
+    assert ss(2048, 8, 6, 4, 4, 256, 64) == 5        # 4 x 8 windowed rows: 48 per group, 3 slices
     assert ss(2048, 8, 6, 4, 1, 256, 64) == 21
     assert ss(2048, 4, 6, 4, 4, 256, 64) == 8        # 24 rows, 2 slices
     assert ss(2048, 8, 6, 4, 16, 256, 64) == 0       # only 1 split would fit
