@@ -84,7 +84,7 @@ def test_reference_cases(ctxs, qlens, nhd, qnc):
         assert math.isfinite(emax) and emax < 4e-3, (ctxs, qlens, ns, emax)
 
 
-def baseline_case(n):
+def benchmark_case(n):
     """The benchmark decode workloads: 1 single token over 4,096 keys, 2 MTP verify (4 tokens)
     over 61,440 keys, 3 four windowed sequences of 8 non-causal tokens (2,048-key window, freed
     pages poisoned), 4 four tokens over 200,000 keys with 1 % outlier rows."""
@@ -103,11 +103,11 @@ def baseline_case(n):
 
 
 @pytest.mark.parametrize("n,nsplit", [(1, 16), (2, 64), (3, 32), (4, 64)])
-def test_baseline_configs(n, nsplit):
-    c = baseline_case(n)
+def test_benchmark_workloads_at_full_size(n, nsplit):
+    c = benchmark_case(n)
     ref, written = oracle_of(c)
     d = c.to("cuda")
-    say(f"config {n} nsplit {nsplit}")
+    say(f"benchmark workload {n} nsplit {nsplit}")
     out = gpu_decode(d, nsplit)
     emax, emean = errors(out, ref, written)
     say(f"  max-abs {emax:.2e} mean-abs {emean:.2e}")
@@ -393,7 +393,7 @@ def test_hip_graph_capture_and_replay():
 def test_hip_graph_of_sliced_rows():
     """The windowed 4 x 8-row batch at 5 splits (three 16-row slices per group) captured in a HIP
     graph: six replays with new queries, each bit-equal to an eager call on the same inputs."""
-    c = baseline_case(3).to("cuda")
+    c = benchmark_case(3).to("cuda")
     T = c.num_tokens
     out = torch.zeros((T, HQ, 256), dtype=torch.float16, device="cuda")
     po, pm, pl = kvc.partial_buffers(T, HQ, NSEG, "cuda")
@@ -432,7 +432,7 @@ def test_config4_graph_replayed_1000_times():
     """Config 4 as specified: the long-context call (200,000 keys, 1 % outlier rows) captured once in
     a HIP graph and replayed 1,000 times. Every 250th replay is compared with the eager call (bit
     for bit) after a device synchronisation; the last one is also held to the oracle."""
-    c = baseline_case(4)
+    c = benchmark_case(4)
     ref, written = oracle_of(c)
     d = c.to("cuda")
     T = d.num_tokens
