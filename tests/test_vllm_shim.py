@@ -134,6 +134,19 @@ MEASURED_BEST = [
 ]
 
 
+def test_limits_match_the_operator_source():
+    """The shim mirrors two limits of the decode operator: the rows per kv head it accepts
+    (16 x kMaxRowBlocks) and the sequences x window up to which it slices row groups
+    (kSliceKeys). Both are read from the operator's source so the two cannot drift apart."""
+    import os
+    import re
+    src = open(os.path.join(os.path.dirname(shim.__file__), "csrc", "pd_kernels.hpp")).read()
+    blocks = int(re.search(r"constexpr int kMaxRowBlocks = (\d+);", src).group(1))
+    keys = int(re.search(r"constexpr int64_t kSliceKeys = (\d+);", src).group(1))
+    assert shim.MAX_ROWS_PER_KV_HEAD == 16 * blocks
+    assert shim.SLICE_KEYS == keys
+
+
 def test_sliced_splits_rule():
     """Windowed groups of more than 16 rows: the largest split count at which slices of 16 rows
     still fill one round of workgroups, if at least 2 (else 0: the makespan model decides)."""
