@@ -287,6 +287,18 @@ def test_prefill_rejects_sizes_beyond_32_bits(lib, entry):
     assert rc == 1 and "below 2^31" in err.value.decode(), (rc, err.value)
 
 
+def test_prefill_model_constants_match_the_kernel_source():
+    """The split-count model in pth_dec mirrors two prefill kernel constants: the query rows per
+    workgroup (kFaRows) and the entries of its LDS block table (kFaBt)."""
+    csrc = os.path.join(os.path.dirname(pth_dec.__file__), "csrc")
+    hpp = open(os.path.join(csrc, "pd_kernels.hpp")).read()
+    waves = int(re.search(r"constexpr int kFaWaves = (\d+);", hpp).group(1))
+    rb = int(re.search(r"constexpr int kFaRB = (\d+);", hpp).group(1))
+    bt = int(re.search(r"constexpr int kFaBt = (\d+);", open(os.path.join(csrc, "pd_prefill.hip")).read()).group(1))
+    assert pth_dec.PREFILL_ROWS_PER_WORKGROUP == waves * rb * 16
+    assert pth_dec.PREFILL_LDS_TABLE == bt
+
+
 def test_prefill_split_count_policy():
     """pth_dec.prefill_splits picks the count that the makespan model rates fastest. Each pin below
     is the count that was fastest on an MI355X (graph replays, 24 q / 4 kv heads over 61,440
