@@ -302,6 +302,21 @@ def test_windowed_row_slices(hq, ctxs, qlens, window, causal):
         assert emax <= 2e-3 and emean <= 2e-4, (ns, emax, emean)
 
 
+def test_row_slices_at_the_one_round_boundary():
+    """4 windowed sequences x 4 query tokens (24 rows per kv head, 2 slices): on a 256-CU device 8
+    splits fill exactly one round of sliced workgroups (8 x 4 x 4 x 2 = 256) and 9 do not (then
+    unsliced); both meet the bar, whichever the device's count makes them."""
+    c = kvc.make_case([3000, 2100, 7000, 40], [4, 4, 3, 4], num_q_heads=HQ, num_kv_heads=HKV, block_size=16,
+                      seed=321, window=2048, causal=True, poison=True)
+    ref, written = oracle_of(c)
+    d = c.to("cuda")
+    for ns in (8, 9):
+        say(f"row slices at the boundary nsplit={ns}")
+        out = gpu_decode(d, ns)
+        emax, emean = errors(out, ref, written)
+        assert math.isfinite(emax) and emax <= 2e-3 and emean <= 2e-4, (ns, emax, emean)
+
+
 def test_padding_tokens_untouched():
     c = kvc.make_case([300, 40], [4, 2], num_q_heads=HQ, num_kv_heads=HKV, block_size=16, seed=8)
     d = c.to("cuda")
